@@ -1,0 +1,118 @@
+// common.hpp -- internal contract of the MI355X grouped Ozaki-II DGEMM library.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "ggemm.h"
+#include "ggemm_graph.h"
+#include "ggemm_oz2.h"
+
+namespace ggemm {
+
+constexpr int kMaxModuli = GGEMM_MAX_MODULI;
+constexpr int kMaxPlanes = kMaxModuli + OZ2_EXTRA_PLANES;   // residues + abs plane
+constexpr int kPow2Table = 128;                             // 2^e mod p tabulated for e < 128
+constexpr int kS2Bits = 18;                                 // fractional bits of s2
+constexpr int kKpAlign = 32;                                // Kp = round_up(k, 32)
+constexpr size_t kBufAlign = 256;                           // byte alignment of every block
+
+inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+inline int kp_of(int k) { return (int)align_up((size_t)k, kKpAlign); }
+
+// CRT constants for N = 1..20 moduli (the quantities of src/moduli.h:43-58), built on the host
+// with exact big-integer arithmetic and copied once per device into global memory.
+struct CrtTables {
+  int32_t p[kMaxModuli];
+  uint32_t magic[kMaxModuli];                  // floor(2^32 / p)
+  uint8_t pow2[kMaxModuli][kPow2Table];        // 2^e mod p
+  uint64_t s1[kMaxModuli + 1][kMaxModuli];     // floor(M_l / u1)
+  uint32_t s2[kMaxModuli + 1][kMaxModuli];     // round(frac(M_l / u1) 2^18)
+  int32_t qinv[kMaxModuli + 1][kMaxModuli];    // M_l^-1 mod p_l
+  int64_t P1[kMaxModuli + 1];                  // floor(P / u1)
+  double P2[kMaxModuli + 1];                   // frac(P / u1)
+  double inv_Pu[kMaxModuli + 1];               // u1 / P
+  int32_t log2_u1[kMaxModuli + 1];
+  double T[kMaxModuli + 1];                    // per-row / per-column 2-norm budget
+  double log2P[kMaxModuli + 1];
+};
+
+// Host tables (built once per process); returns nullptr if the moduli are inconsistent.
+const CrtTables* host_tables();
+
+// Process-wide per-device state: the tables and the four sticky counters
+// {nonfinite vectors, uncertified, repaired, safety fallback}.  Created on first use on the
+// current device and kept until the process ends.
+struct DevCtx {
+  int device;
+  int num_cus;
+  const CrtTables* tab;             // device copy
+  unsigned long long* counters;     // device, 4 entries
+};
+DevCtx* dev_ctx();                  // current device; nullptr on failure
+
+// Native FP64 problem descriptor (device-resident so a captured graph can be re-pointed).
+struct F64Problem {
+  int m, n, k, lda, ldb, ldc;
+  const double* A;
+  const double* B;
+  double* C;
+  double alpha, beta;
+};
+
+// Schedule image shared by the tile-based kernels (INT8 GEMM, FP64 GEMM):
+//   int[0] total tiles, int[1] entries, int[2..7] reserved,
+//   prefix[entries + 1] (first tile of each entry), entry[entries] = (problem << 2) | cfg.
+constexpr int kSchedHdr = 8;
+inline size_t sched_bytes(int entries) {
+  return sizeof(int) * (size_t)(kSchedHdr + 2 * (size_t)entries + 1 + 8);
+}
+
+// INT8 GEMM tile configurations (edge of the square output tile).
+constexpr int kI8NumCfg = 3;
+inline int i8_tile_edge(int cfg) { return cfg == 0 ? 128 : (cfg == 1 ? 64 : 32); }
+// Builds the INT8 schedule (LPT order); cfg < 0 in a problem selects automatically.
+int i8_build_schedule(const i8_problem* h, int num, void* h_ws, size_t ws_bytes, i8_sched_info* info,
+                      int num_cus);
+int i8_launch(const i8_problem* d_probs, const void* d_sched, const i8_sched_info* info, hipStream_t s);
+
+// FP64 MFMA grouped GEMM (native routes).  h_ws receives the schedule image.
+int f64_build_schedule(const F64Problem* h, int num, void* h_ws, size_t ws_bytes, int* total_tiles,
+                       size_t* bytes_used);
+int f64_launch(const F64Problem* d_probs, const void* d_sched, int total_tiles, hipStream_t s);
+
+// Launchers used by the orchestration (return 0 on success).
+int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t s);
+int recon_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t s, int mode);
+
+}  // namespace ggemm
+
+// ----------------------------------------------------------------------------- handle
+struct ggemm_handle_s {
+  hipStream_t stream;
+  int device, num_cus;
+  int max_problems;
+  size_t max_A_elems, max_B_elems, max_C_elems;
+  int min_k;
+
+  int8_t* A8; size_t A8_bytes;
+  int8_t* B8; size_t B8_bytes;
+  int32_t* C32; size_t C32_bytes;
+  int32_t* row_shift; size_t row_shift_elems;
+  int32_t* col_shift; size_t col_shift_elems;
+
+  // one device descriptor blob mirrored by two pinned host slots (double-buffered)
+  void* h_desc; void* d_desc; size_t desc_bytes;
+  hipEvent_t desc_done[2]; int desc_next;
+
+  // host scratch sized at create
+  ggemm_plan_entry_t* plan;
+  int* plan_memo; size_t plan_memo_cap;
+  int* emu_idx; int* nat_idx;
+  i8_sched_info* loop_info;
+
+  ggemm_device_model_t dm;
+  int ws_diag_printed;
+  int stats_repair;
+};

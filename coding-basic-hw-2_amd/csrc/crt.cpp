@@ -1,0 +1,231 @@
+// crt.cpp -- CRT constants (host), per-device context, a-priori error bound and moduli choice,
+// device counters.
+//
+// The quantities follow the reference's src/moduli.h:8-21 and :124-181 (moduli set, M_l split
+// into s1 + s2 2^-18 against u1 = 2^sh, P1/P2, T_N) and src/ozaki2_numerics.cu:639-693 (bound,
+// choice of N, counters).  The big-integer arithmetic here is this library's own 64-bit-limb
+// code; only the conversion of P to double keeps the reference's exact operation order (Horner
+// over 32-bit limbs in 80-bit long double) because T_N, and with it every shift, depends on it
+// to the last bit.
+#include <cmath>
+#include <cstring>
+#include <mutex>
+
+#include "common.hpp"
+
+namespace ggemm {
+namespace {
+
+// src/moduli.h:39-41
+constexpr int kModuli[kMaxModuli] = {256, 255, 253, 251, 247, 239, 233, 229, 227, 223,
+                                     217, 211, 199, 197, 193, 191, 181, 179, 173, 167};
+
+// Unsigned integer below 2^192 as three 64-bit limbs (P_20 < 2^155).
+struct U192 {
+  uint64_t w[3] = {0, 0, 0};
+};
+U192 mul_small(U192 a, uint32_t m) {
+  unsigned __int128 c = 0;
+  for (auto& x : a.w) {
+    c += (unsigned __int128)x * m;
+    x = (uint64_t)c;
+    c >>= 64;
+  }
+  return a;
+}
+uint32_t divmod_small(U192 a, uint32_t d, U192* q) {
+  unsigned __int128 r = 0;
+  U192 out;
+  for (int i = 2; i >= 0; --i) {
+    unsigned __int128 cur = (r << 64) | a.w[i];
+    out.w[i] = (uint64_t)(cur / d);
+    r = cur % d;
+  }
+  if (q) *q = out;
+  return (uint32_t)r;
+}
+int bit_length(const U192& a) {
+  for (int i = 2; i >= 0; --i)
+    if (a.w[i]) return 64 * i + 64 - __builtin_clzll(a.w[i]);
+  return 0;
+}
+int test_bit(const U192& a, int i) { return (i < 0 || i >= 192) ? 0 : (int)((a.w[i / 64] >> (i % 64)) & 1); }
+// a >> s for s >= 0, a << -s for s < 0 (bits beyond 192 dropped)
+U192 shift(const U192& a, int s) {
+  U192 r;
+  for (int i = 0; i < 192; ++i)
+    if (test_bit(a, i)) {
+      const int j = i - s;
+      if (j >= 0 && j < 192) r.w[j / 64] |= 1ull << (j % 64);
+    }
+  return r;
+}
+U192 low_bits(const U192& a, int s) {
+  U192 r;
+  for (int i = 0; i < s && i < 192; ++i)
+    if (test_bit(a, i)) r.w[i / 64] |= 1ull << (i % 64);
+  return r;
+}
+// P as a double: Horner over 32-bit limbs, most significant first, in long double.
+double to_double(const U192& a) {
+  long double v = 0.0L;
+  for (int i = 5; i >= 0; --i) {
+    const uint32_t limb = (uint32_t)(a.w[i / 2] >> (32 * (i % 2)));
+    v = v * 4294967296.0L + (long double)limb;
+  }
+  return (double)v;
+}
+
+int build(CrtTables* t) {
+  std::memset(t, 0, sizeof *t);
+  for (int a = 0; a < kMaxModuli; ++a)
+    for (int b = a + 1; b < kMaxModuli; ++b) {
+      int x = kModuli[a], y = kModuli[b];
+      while (y) { const int r = x % y; x = y; y = r; }
+      if (x != 1) return 1;
+    }
+  for (int l = 0; l < kMaxModuli; ++l) {
+    const uint32_t p = (uint32_t)kModuli[l];
+    t->p[l] = (int32_t)p;
+    t->magic[l] = (uint32_t)((1ull << 32) / p);
+    uint32_t v = 1 % p;
+    for (int e = 0; e < kPow2Table; ++e) { t->pow2[l][e] = (uint8_t)v; v = (2 * v) % p; }
+  }
+  for (int N = 1; N <= kMaxModuli; ++N) {
+    U192 P;
+    P.w[0] = 1;
+    for (int l = 0; l < N; ++l) P = mul_small(P, (uint32_t)kModuli[l]);
+    U192 M[kMaxModuli];
+    int top = 0;
+    for (int l = 0; l < N; ++l) {
+      const uint32_t p = (uint32_t)kModuli[l];
+      if (divmod_small(P, p, &M[l]) != 0) return 3;
+      const uint32_t mr = divmod_small(M[l], p, nullptr);
+      int inv = -1;
+      for (uint32_t x = 0; x < p; ++x)
+        if ((mr * x) % p == 1 % p) { inv = (int)x; break; }
+      if (inv < 0) return 4;
+      t->qinv[N][l] = inv;
+      top = std::max(top, bit_length(M[l]));
+    }
+    const int sh = top - 49;   // u1 = 2^sh keeps every M_l / u1 below 2^49
+    t->log2_u1[N] = sh;
+    for (int l = 0; l < N; ++l) {
+      t->s1[N][l] = shift(M[l], sh).w[0];
+      uint64_t s2 = 0;
+      if (sh > 0) {
+        const U192 frac = low_bits(M[l], sh);
+        if (sh >= kS2Bits)   // round half up to 18 fractional bits
+          s2 = shift(frac, sh - kS2Bits).w[0] + (uint64_t)test_bit(frac, sh - kS2Bits - 1);
+        else
+          s2 = frac.w[0] << (kS2Bits - sh);
+      }
+      if (s2 > (1u << kS2Bits) || t->s1[N][l] >= (1ull << 49)) return 5;
+      t->s2[N][l] = (uint32_t)s2;
+    }
+    const U192 P1 = shift(P, sh);
+    if (bit_length(P1) > 57) return 7;
+    t->P1[N] = (int64_t)P1.w[0];
+    t->P2[N] = sh > 0 ? std::ldexp(to_double(low_bits(P, sh)), -sh) : 0.0;
+    t->inv_Pu[N] = 1.0 / ((double)t->P1[N] + t->P2[N]);
+    const double Pd = to_double(P);
+    t->log2P[N] = std::log2(Pd);
+    t->T[N] = std::sqrt(Pd * 0.5 * (1.0 - std::ldexp(1.0, -20))) * (1.0 - std::ldexp(1.0, -40));
+  }
+  return 0;
+}
+
+std::mutex g_ctx_mu;
+DevCtx* g_ctx[64] = {};
+
+}  // namespace
+
+const CrtTables* host_tables() {
+  static CrtTables tab;
+  static const int st = build(&tab);
+  return st == 0 ? &tab : nullptr;
+}
+
+DevCtx* dev_ctx() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lk(g_ctx_mu);
+  if (g_ctx[dev]) return g_ctx[dev];
+  const CrtTables* h = host_tables();
+  if (!h) return nullptr;
+  DevCtx* c = new DevCtx{};
+  c->device = dev;
+  if (hipDeviceGetAttribute(&c->num_cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      c->num_cus <= 0)
+    c->num_cus = 256;
+  void* tab = nullptr;
+  void* cnt = nullptr;
+  if (hipMalloc(&tab, sizeof(CrtTables)) != hipSuccess ||
+      hipMalloc(&cnt, 4 * sizeof(unsigned long long)) != hipSuccess ||
+      hipMemcpy(tab, h, sizeof(CrtTables), hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemset(cnt, 0, 4 * sizeof(unsigned long long)) != hipSuccess) {
+    if (tab) (void)hipFree(tab);
+    if (cnt) (void)hipFree(cnt);
+    delete c;
+    return nullptr;
+  }
+  c->tab = static_cast<const CrtTables*>(tab);
+  c->counters = static_cast<unsigned long long*>(cnt);
+  g_ctx[dev] = c;
+  return c;
+}
+
+}  // namespace ggemm
+
+using namespace ggemm;
+
+extern "C" int oz2_init_constants(void) { return dev_ctx() ? 0 : 1; }
+
+// src/ozaki2_numerics.cu:639-650: eps_N(k) = 4 sqrt(k)/T + 4k/T^2 + 4 u1 (N 255 2^-19 + 2^-10)/T^2 + u
+extern "C" double oz2_error_bound(int k, int num_moduli) {
+  const CrtTables* t = host_tables();
+  if (!t || num_moduli < 1 || num_moduli > kMaxModuli || k < 0) return INFINITY;
+  const double T = t->T[num_moduli];
+  const double T2 = T * T;
+  const double kk = (double)k;
+  const double u = std::ldexp(1.0, -53);
+  const double u1 = std::ldexp(1.0, t->log2_u1[num_moduli]);
+  return 4.0 * std::sqrt(kk) / T + 4.0 * kk / T2 +
+         4.0 * u1 * (num_moduli * 255.0 * std::ldexp(1.0, -19) + std::ldexp(1.0, -10)) / T2 + u;
+}
+
+// src/ozaki2_numerics.cu:652-657
+extern "C" int oz2_choose_num_moduli(int k, double target_rel_err) {
+  if (k < 0 || k > OZ2_MAX_K) return -1;
+  for (int N = 2; N <= kMaxModuli; ++N)
+    if (oz2_error_bound(k, N) <= target_rel_err) return N;
+  return -1;
+}
+
+// src/ozaki2_numerics.cu:665-673
+extern "C" int oz2_choose_num_moduli_cw(int k, double rho_budget) {
+  if (k < 0 || k > OZ2_MAX_K) return -1;
+  if (rho_budget < 1.0) rho_budget = 1.0;
+  const double u = std::ldexp(1.0, -53);
+  const double budget = 0.5 * (k > 2 ? (double)(k - 2) : 1.0) * u;
+  for (int N = 2; N <= kMaxModuli; ++N)
+    if ((oz2_error_bound(k, N) - u) * rho_budget <= budget) return N;
+  return kMaxModuli;
+}
+
+// src/ozaki2_numerics.cu:675-693
+extern "C" int oz2_read_counters(oz2_counters* out, int reset, hipStream_t s) {
+  DevCtx* c = dev_ctx();
+  if (!c) return 1;
+  unsigned long long h[4] = {0, 0, 0, 0};
+  if (out && hipMemcpyAsync(h, c->counters, sizeof h, hipMemcpyDeviceToHost, s) != hipSuccess) return 2;
+  if (reset && hipMemsetAsync(c->counters, 0, sizeof h, s) != hipSuccess) return 4;
+  if (out) {
+    if (hipStreamSynchronize(s) != hipSuccess) return 3;
+    out->nonfinite_vectors = h[0];
+    out->uncertified = h[1];
+    out->repaired = h[2];
+    out->safety_fallback = h[3];
+  }
+  return 0;
+}

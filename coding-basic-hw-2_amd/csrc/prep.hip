@@ -1,0 +1,422 @@
+// prep.hip -- Ozaki-II residue preparation for a whole group (one launch).
+//
+// Per problem (alpha != 0, N moduli):
+//   s_i   = largest s with 2^s ||A(i,:)||_2 (1+2^-30)^(1/2) <= T_N   (t_j likewise for B(:,j))
+//   A'    = trunc(2^s A)                      (toward zero, so ||A'_i|| <= T_N)
+//   plane l < N : sym(A' mod p_l) in [-(p-1)/2, (p-1)/2]   (p = 256: [-128, 127])
+//   plane N     : floor(2^sigma |A|) in [0, 127], sigma = 6 - ilogb(max_k |A_ik|)
+//   workspace   : {s, sigma, ||2^s A - A'|| float-rounded-up, ||A'|| float-rounded-up}
+// following src/ozaki2_numerics.cu:112-231 (element arithmetic) and :242-442 (kernel).
+// Rows / columns with NaN/Inf get s = OZ2_SHIFT_NONFINITE (zero residues); all-zero ones get
+// sigma = OZ2_SHIFT_ZERO.
+//
+// Bit-exactness of s, sigma and the two norm bounds requires the reference's summation order:
+//   A rows   : 8 chains, chain c = k (mod 8) accumulated in ascending k with fma, then the chain
+//              sums added c = 0..7 (src/ozaki2_numerics.cu:274-305, :356-363);
+//   B columns: 32 chains k = L (mod 32) for the norm; for the residue-pass sums lane L owns
+//              k = 4L + 128c + e (c ascending, e = 0..3); lane values combined by the XOR
+//              butterfly o = 16, 8, 4, 2, 1 (src/ozaki2_numerics.cu:373-440).
+// Everything else (residues, abs plane) is elementwise and mapped freely for the hardware:
+//   * A (column-major in HBM, row-major residues out): a block owns 32 rows.  The chain threads
+//     load a 32 x 128 k-tile with 256-byte coalesced reads, keep the ordered chain sums, and
+//     park the doubles in LDS k-major; then every thread takes 16 consecutive k of one row,
+//     computes the residues and writes each plane with one 128-bit store.
+//   * B (column-major = K contiguous): 32 lanes per column, 4 consecutive k per lane: 1 KB
+//     coalesced loads, 128 contiguous residue bytes per plane per store.
+// Floating-point contraction is off in this file: the only fused operations are the explicit
+// fma() calls, which are the reference's own.
+#include <cmath>
+
+#include "common.hpp"
+
+#pragma clang fp contract(off)
+
+namespace ggemm {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kARows = 32;      // rows of A per block
+constexpr int kATile = 128;     // k tile of the A residue pass
+constexpr int kBCols = 8;       // columns of B per block (32 lanes each)
+constexpr int kChains = 8;      // A-row reduction chains
+
+__device__ __forceinline__ double pow2d(int e) {   // 2^e, e in [-1022, 1023]
+  return __longlong_as_double((long long)(e + 1023) << 52);
+}
+// x * 2^e: one exact multiply for |e| <= 1000, else three clamped steps.
+__device__ __forceinline__ double mul_pow2(double x, int e) {
+  if (e >= -1000 && e <= 1000) return x * pow2d(e);
+#pragma unroll
+  for (int r = 0; r < 3; ++r) {
+    const int ee = max(-1000, min(1000, e));
+    x *= pow2d(ee);
+    e -= ee;
+  }
+  return x;
+}
+
+// Largest s with 2^s * nrm <= T, nrm = f 2^(g + add) (frexp), T = F 2^G.
+__device__ __forceinline__ int choose_shift(double nrm, int add, double T) {
+  int g, G;
+  const double f = frexp(nrm, &g);
+  const double F = frexp(T, &G);
+  return G - (g + add) - (f > F ? 1 : 0);
+}
+__device__ __forceinline__ int shift_from_norm(double maxabs, double ssq, bool rescaled, double T) {
+  if (isinf(maxabs) || isnan(ssq)) return OZ2_SHIFT_NONFINITE;
+  if (!(maxabs > 0.0)) return 0;
+  const double nm = sqrt(ssq * (1.0 + 0x1p-30));
+  return choose_shift(nm, rescaled ? ilogb(maxabs) : 0, T);
+}
+__device__ __forceinline__ int abs_shift(double maxabs, int sh) {
+  if (sh == OZ2_SHIFT_NONFINITE) return 0;
+  if (!(maxabs > 0.0)) return OZ2_SHIFT_ZERO;
+  return 6 - ilogb(maxabs);
+}
+__device__ __forceinline__ bool needs_rescale(double maxabs) {
+  return maxabs > 0.0 && (maxabs > 0x1p400 || maxabs < 0x1p-400);
+}
+// Float round-up of sqrt(x (1 + 2^-30)), returned as the float's bit pattern (x >= 0 finite).
+__device__ __forceinline__ int32_t norm_ub_bits(double x) {
+  const double s = sqrt(x * (1.0 + 0x1p-30));
+  float f = (float)s;
+  int32_t b = __float_as_int(f);
+  if ((double)f < s) ++b;   // next float up (f >= 0)
+  return b;
+}
+
+// Residues of an integer-valued double x (|x| < 2^81): x = sign M 2^E with M < 2^53 split in
+// 18-bit chunks; x mod p = sign (c0 [2^E] + c1 [2^(E+18)] + c2 [2^(E+36)]) mod p.
+struct Split {
+  uint32_t c0, c1, c2;
+  int E;
+  bool neg;
+};
+__device__ __forceinline__ Split split_int(double x) {
+  Split d;
+  const double ax = fabs(x);
+  d.neg = x < 0.0;
+  uint64_t M;
+  int E;
+  if (ax < 9007199254740992.0) {
+    M = (uint64_t)ax;
+    E = 0;
+  } else {
+    const uint64_t b = (uint64_t)__double_as_longlong(ax);
+    E = min((int)((b >> 52) & 0x7ff) - 1075, kPow2Table - 37);
+    M = (b & ((1ull << 52) - 1)) | (1ull << 52);
+  }
+  d.c0 = (uint32_t)(M & 0x3ffff);
+  d.c1 = (uint32_t)((M >> 18) & 0x3ffff);
+  d.c2 = (uint32_t)(M >> 36);
+  d.E = E;
+  return d;
+}
+__device__ __forceinline__ uint32_t residue_u8(const Split& d, uint32_t p, uint32_t magic, const uint8_t* pw) {
+  const uint32_t s = d.c0 * pw[d.E] + d.c1 * pw[d.E + 18] + d.c2 * pw[d.E + 36];   // < 2^28
+  uint32_t r = s - __umulhi(s, magic) * p;                                         // < 2p
+  r = r >= p ? r - p : r;
+  if (d.neg && r) r = p - r;
+  const int ri = (int)r > (int)((p - 1) >> 1) ? (int)r - (int)p : (int)r;
+  return (uint32_t)(uint8_t)(int8_t)ri;
+}
+__device__ __forceinline__ uint32_t abs_u8(double a, int sig) {
+  if (sig == OZ2_SHIFT_ZERO) return 0;
+  return (uint32_t)(int)fmin(127.0, trunc(mul_pow2(fabs(a), sig)));
+}
+
+struct PrepShared {
+  uint8_t pow2[kMaxModuli][kPow2Table];
+  uint32_t p[kMaxModuli], magic[kMaxModuli];
+  double red0[kChains][kARows];
+  double red1[kChains][kARows];
+  int shift[kARows], sig[kARows];
+  double rowmax[kARows];
+  double tile[kATile][kARows];      // A values of the current k-tile, k-major
+};
+
+// ------------------------------------------------------------------------------- A rows
+__device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ tab, int blk, int split,
+                          int nsplit, PrepShared& sm, unsigned long long* cnt) {
+  const int tid = threadIdx.x;
+  const int N = pr.num_moduli, K = pr.k, Kp = pr.kp, m = pr.m;
+  const int row0 = blk * kARows;
+  const int r = tid & 31, c = tid >> 5;          // chain role: row r, chain c
+  const int i = row0 + r;
+  const bool valid = i < m;
+  const double* __restrict__ A = pr.A;
+  const size_t lda = (size_t)pr.lda;
+  const double T = tab->T[N];
+
+  // ---- pass 1: row max and sum of squares, chain c = k mod 8 ascending
+  double mx = 0.0, ss = 0.0;
+  if (valid) {
+    int k = c;
+    for (; k + 24 < K; k += 32) {
+      const double a0 = A[i + (size_t)k * lda], a1 = A[i + (size_t)(k + 8) * lda];
+      const double a2 = A[i + (size_t)(k + 16) * lda], a3 = A[i + (size_t)(k + 24) * lda];
+      mx = fmax(fmax(fmax(fmax(mx, fabs(a0)), fabs(a1)), fabs(a2)), fabs(a3));
+      ss = fma(a0, a0, ss); ss = fma(a1, a1, ss); ss = fma(a2, a2, ss); ss = fma(a3, a3, ss);
+    }
+    for (; k < K; k += 8) {
+      const double a = A[i + (size_t)k * lda];
+      mx = fmax(mx, fabs(a));
+      ss = fma(a, a, ss);
+    }
+  }
+  sm.red0[c][r] = mx;
+  __syncthreads();
+  if (c == 0) {
+    double M = 0.0;
+    for (int q = 0; q < kChains; ++q) M = fmax(M, sm.red0[q][r]);
+    sm.rowmax[r] = M;
+  }
+  __syncthreads();
+  const double rowmax = sm.rowmax[r];
+  const bool resc = valid && needs_rescale(rowmax);
+  if (resc) {   // rare: exact power-of-two prescaling so the squares cannot overflow / underflow
+    const int e = -ilogb(rowmax);
+    ss = 0.0;
+    for (int k = c; k < K; k += kChains) {
+      const double a = mul_pow2(A[i + (size_t)k * lda], e);
+      ss = fma(a, a, ss);
+    }
+  }
+  sm.red1[c][r] = ss;
+  __syncthreads();
+  if (c == 0) {
+    double S = 0.0;
+    for (int q = 0; q < kChains; ++q) S += sm.red1[q][r];
+    const int sh = valid ? shift_from_norm(rowmax, S, resc, T) : 0;
+    const int sg = valid ? abs_shift(rowmax, sh) : OZ2_SHIFT_ZERO;
+    sm.shift[r] = sh;
+    sm.sig[r] = sg;
+    if (valid && split == 0) {
+      pr.row_shift[i] = sh;
+      pr.row_shift[m + i] = sg;
+      if (sh == OZ2_SHIFT_NONFINITE) atomicAdd(&cnt[0], 1ull);
+    }
+  }
+  __syncthreads();
+
+  // ---- pass 2: residues of this split's k-tiles; split 0 also walks every tile for the
+  //      ordered ||dA||, ||A'|| chain sums (the residue values do not depend on the split)
+  const int sh_c = sm.shift[r];
+  const bool nf_c = sh_c == OZ2_SHIFT_NONFINITE;
+  const int rr = tid & 31, seg = tid >> 5;   // residue role: row rr, k = 16 seg .. 16 seg + 15
+  const int sh_r = sm.shift[rr], sg_r = sm.sig[rr];
+  const bool nf_r = sh_r == OZ2_SHIFT_NONFINITE;
+  const bool rvalid = row0 + rr < m;
+  double da2 = 0.0, na2 = 0.0;
+  const int ntile = (Kp + kATile - 1) / kATile;
+  const int per = (ntile + nsplit - 1) / nsplit;
+  const int w0 = min(ntile, split * per), w1 = min(ntile, w0 + per);   // tiles written here
+  const int l0 = split == 0 ? 0 : w0, l1 = split == 0 ? ntile : w1;   // tiles walked here
+  for (int t = l0; t < l1; ++t) {
+    const int k0 = t * kATile;
+#pragma unroll 4
+    for (int jj = 0; jj < kATile / kChains; ++jj) {
+      const int kk = c + kChains * jj;
+      const int k = k0 + kk;
+      const double a = (valid && k < K) ? A[i + (size_t)k * lda] : 0.0;
+      if (!nf_c && split == 0) {
+        const double xs = mul_pow2(a, sh_c);
+        const double xt = trunc(xs);
+        const double fr = xs - xt;
+        da2 = fma(fr, fr, da2);
+        na2 = fma(xt, xt, na2);
+      }
+      sm.tile[kk][r] = a;
+    }
+    __syncthreads();
+    const int kb = k0 + 16 * seg;
+    if (t >= w0 && t < w1 && rvalid && kb < Kp) {
+      int8_t* dst = pr.A8 + (size_t)(row0 + rr) * Kp + kb;
+      if (nf_r) {
+        for (int l = 0; l <= N; ++l)
+          *reinterpret_cast<uint4*>(dst + (size_t)l * pr.a8_mod_stride) = make_uint4(0u, 0u, 0u, 0u);
+      } else {
+        Split d[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) d[e] = split_int(trunc(mul_pow2(sm.tile[16 * seg + e][rr], sh_r)));
+        for (int l = 0; l < N; ++l) {
+          const uint32_t p = sm.p[l], mg = sm.magic[l];
+          const uint8_t* pw = sm.pow2[l];
+          uint32_t q[4];
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            q[w] = 0u;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) q[w] |= residue_u8(d[4 * w + e], p, mg, pw) << (8 * e);
+          }
+          *reinterpret_cast<uint4*>(dst + (size_t)l * pr.a8_mod_stride) = make_uint4(q[0], q[1], q[2], q[3]);
+        }
+        uint32_t q[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          q[w] = 0u;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) q[w] |= abs_u8(sm.tile[16 * seg + 4 * w + e][rr], sg_r) << (8 * e);
+        }
+        *reinterpret_cast<uint4*>(dst + (size_t)N * pr.a8_mod_stride) = make_uint4(q[0], q[1], q[2], q[3]);
+      }
+    }
+    __syncthreads();
+  }
+  if (split != 0) return;   // block-uniform
+  sm.red0[c][r] = da2;
+  sm.red1[c][r] = na2;
+  __syncthreads();
+  if (c == 0 && valid) {
+    double D = 0.0, Nn = 0.0;
+    for (int q = 0; q < kChains; ++q) { D += sm.red0[q][r]; Nn += sm.red1[q][r]; }
+    pr.row_shift[2 * m + i] = norm_ub_bits(D);
+    pr.row_shift[3 * m + i] = norm_ub_bits(Nn);
+  }
+}
+
+// ---------------------------------------------------------------------------- B columns
+__device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ tab, int blk, int split,
+                          int nsplit, PrepShared& sm, unsigned long long* cnt) {
+  const int lane = threadIdx.x & 31, w = threadIdx.x >> 5;
+  const int j = blk * kBCols + w;
+  const int n = pr.n, N = pr.num_moduli, K = pr.k, Kp = pr.kp;
+  if (j >= n) return;   // no barriers below; the 32-lane group is column-uniform
+  const double* __restrict__ b = pr.B + (size_t)j * pr.ldb;
+  const double T = tab->T[N];
+
+  double mx = 0.0, ss = 0.0;
+  for (int k = lane; k < K; k += 32) {
+    const double a = b[k];
+    mx = fmax(mx, fabs(a));
+    ss = fma(a, a, ss);
+  }
+#pragma unroll
+  for (int o = 16; o; o >>= 1) mx = fmax(mx, __shfl_xor(mx, o, 32));
+  const bool resc = needs_rescale(mx);
+  if (resc) {
+    const int e = -ilogb(mx);
+    ss = 0.0;
+    for (int k = lane; k < K; k += 32) {
+      const double a = mul_pow2(b[k], e);
+      ss = fma(a, a, ss);
+    }
+  }
+#pragma unroll
+  for (int o = 16; o; o >>= 1) ss += __shfl_xor(ss, o, 32);
+  const int sh = shift_from_norm(mx, ss, resc, T);
+  const int sg = abs_shift(mx, sh);
+  if (lane == 0 && split == 0) {
+    pr.col_shift[j] = sh;
+    pr.col_shift[n + j] = sg;
+    if (sh == OZ2_SHIFT_NONFINITE) atomicAdd(&cnt[0], 1ull);
+  }
+  const bool nf = sh == OZ2_SHIFT_NONFINITE;
+
+  double da2 = 0.0, na2 = 0.0;
+  int8_t* base = pr.B8 + (size_t)j * Kp;
+  const int nchunk = (Kp + 127) / 128;
+  const int per = (nchunk + nsplit - 1) / nsplit;
+  const int c0 = min(nchunk, split * per), c1 = min(nchunk, c0 + per);
+  // split 0 walks every chunk (ordered sums) but writes residues only for its own range
+  for (int ch = (split == 0 ? 0 : c0); ch < (split == 0 ? nchunk : c1); ++ch) {
+    const int k0 = 128 * ch + 4 * lane;
+    if (k0 >= Kp) continue;
+    double a[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) a[e] = (k0 + e < K) ? b[k0 + e] : 0.0;
+    const bool write = ch >= c0 && ch < c1;
+    if (nf) {
+      if (write)
+        for (int l = 0; l <= N; ++l) *reinterpret_cast<uint32_t*>(base + (size_t)l * pr.b8_mod_stride + k0) = 0u;
+      continue;
+    }
+    Split d[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const double xs = mul_pow2(a[e], sh);
+      const double xt = trunc(xs);
+      const double fr = xs - xt;
+      if (split == 0) {
+        da2 = fma(fr, fr, da2);
+        na2 = fma(xt, xt, na2);
+      }
+      d[e] = split_int(xt);
+    }
+    if (!write) continue;
+    for (int l = 0; l < N; ++l) {
+      const uint32_t p = sm.p[l], mg = sm.magic[l];
+      const uint8_t* pw = sm.pow2[l];
+      uint32_t q = 0u;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) q |= residue_u8(d[e], p, mg, pw) << (8 * e);
+      *reinterpret_cast<uint32_t*>(base + (size_t)l * pr.b8_mod_stride + k0) = q;
+    }
+    uint32_t q = 0u;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) q |= abs_u8(a[e], sg) << (8 * e);
+    *reinterpret_cast<uint32_t*>(base + (size_t)N * pr.b8_mod_stride + k0) = q;
+  }
+  if (split != 0) return;
+#pragma unroll
+  for (int o = 16; o; o >>= 1) {
+    da2 += __shfl_xor(da2, o, 32);
+    na2 += __shfl_xor(na2, o, 32);
+  }
+  if (lane == 0) {
+    pr.col_shift[2 * n + j] = norm_ub_bits(da2);
+    pr.col_shift[3 * n + j] = norm_ub_bits(na2);
+  }
+}
+
+__global__ void __launch_bounds__(kThreads) prep_kernel(const oz2_problem* __restrict__ probs, int a_blocks,
+                                                        const CrtTables* __restrict__ tab,
+                                                        unsigned long long* __restrict__ cnt) {
+  __shared__ PrepShared sm;
+  const oz2_problem& pr = probs[blockIdx.y];
+  const int N = pr.num_moduli;
+  if (N < 1 || N > kMaxModuli || pr.alpha == 0.0) return;   // alpha == 0: A, B never referenced
+  for (int q = threadIdx.x; q < kMaxModuli * kPow2Table; q += kThreads)
+    (&sm.pow2[0][0])[q] = tab->pow2[q / kPow2Table][q % kPow2Table];
+  if (threadIdx.x < kMaxModuli) {
+    sm.p[threadIdx.x] = (uint32_t)tab->p[threadIdx.x];
+    sm.magic[threadIdx.x] = tab->magic[threadIdx.x];
+  }
+  __syncthreads();
+  const int blk = (int)blockIdx.x;
+  if (blk < a_blocks) {
+    if (blk * kARows >= pr.m) return;
+    prep_rows(pr, tab, blk, blockIdx.z, gridDim.z, sm, cnt);
+  } else {
+    prep_cols(pr, tab, blk - a_blocks, blockIdx.z, gridDim.z, sm, cnt);
+  }
+}
+
+int g_force_split = 0;
+
+}  // namespace
+
+int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t s) {
+  if (num <= 0) return 0;
+  if (num > 65535 || max_m < 0 || max_n < 0) return 1;
+  DevCtx* c = dev_ctx();
+  if (!c) return 2;
+  const int a_blocks = (max_m + kARows - 1) / kARows;
+  const int b_blocks = (max_n + kBCols - 1) / kBCols;
+  if (a_blocks + b_blocks == 0) return 0;
+  const long long blocks = (long long)(a_blocks + b_blocks) * num;
+  const long long target = 4LL * c->num_cus;
+  int S = (int)std::min<long long>(16, std::max<long long>(1, (target + blocks - 1) / blocks));
+  if (g_force_split > 0) S = g_force_split;
+  hipLaunchKernelGGL(prep_kernel, dim3(a_blocks + b_blocks, num, S), dim3(kThreads), 0, s, d, a_blocks,
+                     c->tab, c->counters);
+  return hipGetLastError() == hipSuccess ? 0 : 3;
+}
+
+}  // namespace ggemm
+
+extern "C" int oz2_prep_grouped(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t s) {
+  return ggemm::prep_launch(d, num, max_m, max_n, s);
+}
+
+extern "C" void oz2_debug_force_prep_split(int S) { ggemm::g_force_split = (S >= 1 && S <= 64) ? S : 0; }

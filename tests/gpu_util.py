@@ -1,0 +1,176 @@
+"""Helpers for the GPU parity tests: device buffers through torch (plumbing only) and the
+kernel-level pipeline of the library run on the reference test's host problems."""
+import ctypes as C
+import sys
+
+import numpy as np
+
+import ggemm as G
+import oracle_lib as O
+
+
+def torch():
+    import torch as t
+    return t
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def dev(arr, dtype=None):
+    """numpy -> device tensor (contiguous copy)."""
+    t = torch()
+    a = np.ascontiguousarray(arr)
+    return t.from_numpy(a.copy()).to("cuda")
+
+
+def host(t_):
+    torch().cuda.synchronize()
+    return t_.detach().cpu().numpy()
+
+
+def dev_zeros(nbytes, dtype="uint8"):
+    t = torch()
+    dt = {"uint8": t.uint8, "int8": t.int8, "int32": t.int32, "float64": t.float64}[dtype]
+    itemsize = {"uint8": 1, "int8": 1, "int32": 4, "float64": 8}[dtype]
+    return t.zeros(max(1, (nbytes + itemsize - 1) // itemsize), dtype=dt, device="cuda")
+
+
+def dev_struct_array(structs, ctype):
+    """Copy a list of ctypes structures into device memory; returns the uint8 tensor."""
+    n = max(len(structs), 1)
+    arr = (ctype * n)(*structs)
+    raw = np.frombuffer(bytes(arr), dtype=np.uint8).copy()
+    return dev(raw)
+
+
+def same_bits(a, b):
+    """float64 arrays equal bit for bit, except that any NaN equals any NaN (NaN payloads are
+    not specified by IEEE arithmetic and differ between the host and the GPU)."""
+    a = np.asarray(a, dtype=np.float64)
+    b = np.asarray(b, dtype=np.float64)
+    if a.shape != b.shape:
+        return False
+    both_nan = np.isnan(a) & np.isnan(b)
+    return bool(np.all((a.view(np.int64) == b.view(np.int64)) | both_nan))
+
+
+def read_counters(reset=True):
+    c = G.Oz2Counters()
+    torch().cuda.synchronize()
+    assert G.lib().oz2_read_counters(C.byref(c), 1 if reset else 0, None) == 0
+    return c
+
+
+class WhiteboxRun:
+    """prep -> grouped INT8 GEMM -> reconstruct through the kernel-level ABI for a list of
+    oracle_lib.HostProb, laid out like the reference numerics test (tight planes per problem)."""
+
+    def __init__(self, hs, poison=0x5A):
+        t = torch()
+        self.hs = hs
+        self.dA, self.dB, self.dC = [], [], []
+        self.descs = []
+        a8 = b8 = c32 = rsz = csz = 0
+        for h in hs:
+            kp = O.kp_of(h.k)
+            NP = h.N + 1
+            a8 += NP * h.m * kp
+            b8 += NP * h.n * kp
+            c32 += NP * h.m * h.n
+            rsz += 4 * h.m
+            csz += 4 * h.n
+        self.A8 = t.full((a8 + 16,), poison, dtype=t.uint8, device="cuda")
+        self.B8 = t.full((b8 + 16,), poison, dtype=t.uint8, device="cuda")
+        self.C32 = t.zeros((c32 + 16,), dtype=t.int32, device="cuda")
+        self.rs = t.zeros((rsz + 16,), dtype=t.int32, device="cuda")
+        self.cs = t.zeros((csz + 16,), dtype=t.int32, device="cuda")
+        oa = ob = oc = orr = occ = 0
+        self.offs = []
+        for h in hs:
+            kp = O.kp_of(h.k)
+            NP = h.N + 1
+            A = dev(h.A)
+            B = dev(h.B)
+            Cm = dev(h.C0)
+            self.dA.append(A)
+            self.dB.append(B)
+            self.dC.append(Cm)
+            p = G.Oz2Problem()
+            p.m, p.n, p.k, p.kp, p.num_moduli = h.m, h.n, h.k, kp, h.N
+            p.lda, p.ldb, p.ldc = h.lda, h.ldb, h.ldc
+            p.A, p.B, p.C = A.data_ptr(), B.data_ptr(), Cm.data_ptr()
+            p.alpha, p.beta = h.alpha, h.beta
+            p.A8 = self.A8.data_ptr() + oa
+            p.a8_mod_stride = h.m * kp
+            p.B8 = self.B8.data_ptr() + ob
+            p.b8_mod_stride = h.n * kp
+            p.C32 = self.C32.data_ptr() + 4 * oc
+            p.c32_mod_stride = h.m * h.n
+            p.row_shift = self.rs.data_ptr() + 4 * orr
+            p.col_shift = self.cs.data_ptr() + 4 * occ
+            self.descs.append(p)
+            self.offs.append((oa, ob, oc, orr, occ))
+            oa += NP * h.m * kp
+            ob += NP * h.n * kp
+            oc += NP * h.m * h.n
+            orr += 4 * h.m
+            occ += 4 * h.n
+        self.d_desc = dev_struct_array(self.descs, G.Oz2Problem)
+        self.max_m = max(h.m for h in hs)
+        self.max_n = max(h.n for h in hs)
+
+    def prep(self):
+        rc = G.lib().oz2_prep_grouped(self.d_desc.data_ptr(), len(self.hs), self.max_m, self.max_n, None)
+        assert rc == 0, rc
+
+    def i8_problems(self):
+        probs = []
+        for h, p in zip(self.hs, self.descs):
+            if h.alpha == 0.0:
+                continue
+            for l in range(h.N + 1):
+                probs.append(G.I8Problem(h.m, h.n, p.kp, p.A8 + l * p.a8_mod_stride, p.B8 + l * p.b8_mod_stride,
+                                         p.C32 + 4 * l * p.c32_mod_stride, -1))
+        return probs
+
+    def gemm(self, tile_cfg=-1):
+        probs = self.i8_problems()
+        for q in probs:
+            q.tile_cfg = tile_cfg
+        d_probs = dev_struct_array(probs, G.I8Problem)
+        nb = G.lib().i8_grouped_gemm_sched_ws_bytes(len(probs), 0)
+        ws = dev_zeros(nb)
+        arr = (G.I8Problem * max(len(probs), 1))(*probs)
+        nl = C.c_int(0)
+        rc = G.lib().i8_grouped_gemm_ex(d_probs.data_ptr(), len(probs), arr, ws.data_ptr(), nb, None, C.byref(nl))
+        assert rc == 0, rc
+        torch().cuda.synchronize()
+        return nl.value
+
+    def recon(self, mode):
+        rc = G.lib().oz2_reconstruct_grouped(self.d_desc.data_ptr(), len(self.hs), self.max_m, self.max_n, None, mode)
+        assert rc == 0, rc
+
+    def run(self, mode=G.OZ2_REPAIR_ON):
+        self.prep()
+        self.gemm()
+        self.recon(mode)
+        torch().cuda.synchronize()
+
+    # ---- readback in the oracle's layouts
+    def planes(self, g):
+        h, (oa, ob, oc, orr, occ) = self.hs[g], self.offs[g]
+        kp = O.kp_of(h.k)
+        NP = h.N + 1
+        A8 = host(self.A8[oa:oa + NP * h.m * kp]).view(np.int8)
+        B8 = host(self.B8[ob:ob + NP * h.n * kp]).view(np.int8)
+        C32 = host(self.C32[oc:oc + NP * h.m * h.n])
+        rs = host(self.rs[orr:orr + 4 * h.m])
+        cs = host(self.cs[occ:occ + 4 * h.n])
+        return A8, B8, C32, rs, cs
+
+    def C(self, g):
+        return host(self.dC[g])

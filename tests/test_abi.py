@@ -1,0 +1,198 @@
+"""The C-ABI library on the CPU (no GPU calls): exports, struct layouts, and the host-side
+numerics and planner against the oracle, bit for bit."""
+import ctypes as C
+import json
+import os
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import ggemm as G
+import oracle_lib as O
+
+REPO = Path(__file__).resolve().parents[1]
+GOLDEN = REPO / "tests" / "golden"
+
+
+def _declared_functions():
+    names = set()
+    for h in (REPO / "include").glob("*.h"):
+        txt = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        txt = re.sub(r"//.*", "", txt)
+        for m in re.finditer(r"\b([a-z][a-z0-9_]*)\s*\(", txt):
+            name = m.group(1)
+            if name.startswith(("ggemm_", "oz2_", "i8_")) and not name.endswith("_t"):
+                names.add(name)
+    return names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = G.lib()
+    declared = _declared_functions()
+    assert len(declared) >= 25
+    missing = [n for n in sorted(declared) if not hasattr(lib, n)]
+    assert not missing, missing
+    bound = {s[0] for s in G.SIGNATURES}
+    assert declared <= bound | {"static_assert"}, declared - bound
+
+
+def test_struct_layouts_match_header():
+    assert C.sizeof(G.Problem) == 80
+    assert C.sizeof(G.Config) == 24
+    assert C.sizeof(G.Stats) == 64
+    assert C.sizeof(G.Oz2Problem) == 136
+    assert C.sizeof(G.I8Problem) == 48
+    assert C.sizeof(G.PlanEntry) == 32
+    assert C.sizeof(G.DeviceModel) == 40
+
+
+def test_host_numerics_match_oracle_bitwise():
+    lib, ora = G.lib(), O.oracle()
+    for N in range(1, 21):
+        for k in [0, 1, 16, 17, 31, 32, 100, 1000, 1024, 2245, 2246, 4096, 5646, 5647, 16384, 65536, 131040]:
+            a, b = lib.oz2_error_bound(k, N), ora.oz2o_error_bound(k, N)
+            assert np.float64(a).view(np.int64) == np.float64(b).view(np.int64), (k, N)
+    for k in list(range(0, 64)) + [100, 1000, 2245, 2246, 5646, 5647, 65536, 131040, 131041, -1]:
+        for tgt in (1e-15, 1e-12, 1e-40):
+            assert lib.oz2_choose_num_moduli(k, tgt) == ora.oz2o_choose_num_moduli(k, tgt), (k, tgt)
+        for rho in (1.0, 16.0, 1e6):
+            assert lib.oz2_choose_num_moduli_cw(k, rho) == ora.oz2o_choose_num_moduli_cw(k, rho), (k, rho)
+
+
+def _model(path=None, name=b"gfx950:sramecc+:xnack-", sms=256):
+    old = os.environ.get("GGEMM_CALIB_JSON")
+    if path:
+        os.environ["GGEMM_CALIB_JSON"] = str(path)
+    else:
+        os.environ.pop("GGEMM_CALIB_JSON", None)
+    try:
+        dm = G.DeviceModel()
+        G.lib().ggemm_device_model_init(C.byref(dm), name, 9, 5, sms)
+        return dm
+    finally:
+        if old is None:
+            os.environ.pop("GGEMM_CALIB_JSON", None)
+        else:
+            os.environ["GGEMM_CALIB_JSON"] = old
+
+
+def test_device_model_calibration_sources():
+    nom = _model(name=b"Planner Unit Test GPU (no params file)")
+    assert nom.fp64_flops > 0 and nom.int8_ops > 0 and nom.mem_bw > 0
+    mi = _model()
+    assert mi.fp64_flops == 78.6e12 * 0.8 and mi.int8_ops == 5.03e15 * 0.5 and mi.mem_bw == 8e12 * 0.8
+    miss = _model(GOLDEN / "does_not_exist.json")
+    assert (miss.fp64_flops, miss.int8_ops, miss.mem_bw) == (mi.fp64_flops, mi.int8_ops, mi.mem_bw)
+    nonum = _model(GOLDEN / "planner_no_numbers.json")
+    assert (nonum.fp64_flops, nonum.int8_ops, nonum.mem_bw) == (mi.fp64_flops, mi.int8_ops, mi.mem_bw)
+    v = _model(GOLDEN / "planner_valid.json", sms=132)
+    assert (v.fp64_flops, v.int8_ops, v.mem_bw, v.num_sms) == (5.0e13, 1.0e15, 3.0e12, 132)
+    bad = _model(GOLDEN / "planner_bad_units.json")
+    assert bad.fp64_flops != 67.0 and bad.int8_ops != 1979.0 and bad.mem_bw != 3.35
+    os.environ["GGEMM_FP64_FLOPS"] = "1.5e13"
+    try:
+        e = _model(GOLDEN / "planner_valid.json")
+        assert e.fp64_flops == 1.5e13 and e.int8_ops == 1.0e15
+    finally:
+        del os.environ["GGEMM_FP64_FLOPS"]
+
+
+def _valid_dm():
+    return _model(GOLDEN / "planner_valid.json", name=b"NVIDIA H200", sms=132)
+
+
+def _cfg(nm=0, fb=1, tgt=1e-15):
+    return G.Config(nm, tgt, fb, 0)
+
+
+def _plan_lib(probs, cfg, path, dm, memo=False):
+    arr = G.problems_array(probs)
+    out = (G.PlanEntry * max(len(probs), 1))()
+    if memo:
+        cap = G.lib().ggemm_plan_memo_cap(len(probs))
+        mem = (C.c_int * cap)()
+        rc = G.lib().ggemm_plan_ex(arr, len(probs), C.byref(cfg), path, C.byref(dm), out, mem, cap)
+    else:
+        rc = G.lib().ggemm_plan(arr, len(probs), C.byref(cfg), path, C.byref(dm), out)
+    return rc, out
+
+
+def _plan_oracle(probs, cfg, path, dm):
+    shapes = (O.Shape * max(len(probs), 1))(*[O.Shape(p.m, p.n, p.k, p.alpha, p.beta) for p in probs])
+    odm = O.DeviceModel(dm.num_sms, dm.fp64_flops, dm.int8_ops, dm.mem_bw, dm.tiny_mnk)
+    out = (O.PlanEntry * max(len(probs), 1))()
+    rc = O.oracle().oz2o_plan(shapes, len(probs), cfg.num_moduli, cfg.target_rel_err, cfg.allow_fallback, path,
+                              C.byref(odm), 16.0, out)
+    return rc, out
+
+
+def _random_group(G_, seed):
+    rng = np.random.default_rng(seed)
+    probs = []
+    for _ in range(G_):
+        r = int(rng.integers(0, 100))
+        m, n, k = int(rng.integers(1, 2049)), int(rng.integers(1, 2049)), int(rng.integers(1, 8193))
+        if r < 3:
+            k = 0
+        elif r < 5:
+            m = 0
+        elif r < 7:
+            k = G.MAX_K_EXACT + int(rng.integers(1, 1001))
+        elif r < 12:
+            k = int(rng.integers(1, 17))
+        probs.append(G.Problem(m, n, k, None, max(1, m), None, max(1, k), None, max(1, m),
+                               0.0 if r == 50 else 1.0, 1.0 if r & 1 else 0.0))
+    return probs
+
+
+def _same(a, b):
+    return (a.route == b.route and a.num_moduli == b.num_moduli and a.tile_cfg == b.tile_cfg and
+            np.float64(a.t_emu_s).view(np.int64) == np.float64(b.t_emu_s).view(np.int64) and
+            np.float64(a.t_native_s).view(np.int64) == np.float64(b.t_native_s).view(np.int64))
+
+
+def test_planner_route_table():
+    dm = _valid_dm()
+    for c in json.loads((GOLDEN / "planner_routes.json").read_text())["cases"]:
+        p = G.Problem(c["m"], c["n"], c["k"], None, max(1, c["m"]), None, max(1, c["k"]), None, max(1, c["m"]),
+                      c.get("alpha", 1.0), c.get("beta", 0.0))
+        rc, out = _plan_lib([p], _cfg(c["nm"], c["fb"]), c["path"], dm)
+        assert rc == c["rc"], c["name"]
+        if rc == 0:
+            if c["route"] < 0:
+                assert out[0].route != 7, c["name"]
+            else:
+                assert out[0].route == c["route"], c["name"]
+
+
+@pytest.mark.parametrize("n_probs", [1, 17, 1000, 20000])
+def test_planner_matches_oracle_and_memo(n_probs):
+    """ggemm_plan == oracle plan bit for bit (routes, N, tiles, cost doubles), and the shape memo
+    reproduces the unmemoised plan (tests/test_planner.cpp:367-426)."""
+    for dmi, dm in enumerate([_valid_dm(), _model()]):
+        for variant in (0, 1):
+            probs = _random_group(n_probs, 1000 * n_probs + 10 * dmi + variant)
+            if variant:
+                probs = [probs[g % 7] for g in range(n_probs)]
+            for path in (G.PATH_AUTO, G.PATH_EMU_GROUPED, G.PATH_EMU_LOOP):
+                for cfg in (_cfg(0, 1), _cfg(0, 0), _cfg(9, 1), _cfg(0, 1, 1e-40)):
+                    rl, el = _plan_lib(probs, cfg, path, dm)
+                    rm, em = _plan_lib(probs, cfg, path, dm, memo=True)
+                    ro, eo = _plan_oracle(probs, cfg, path, dm)
+                    assert rl == ro == rm, (path, cfg.num_moduli, cfg.allow_fallback)
+                    if rl == 0:
+                        for g in range(n_probs):
+                            assert _same(el[g], eo[g]), (g, path)
+                            assert _same(el[g], em[g]), (g, path)
+
+
+def test_tiny_route_env():
+    dm = _valid_dm()
+    p = G.Problem(24, 24, 24, None, 24, None, 24, None, 24, 1.0, 0.0)
+    rc, out = _plan_lib([p], _cfg(0, 1), G.PATH_AUTO, dm)
+    assert out[0].route == 4   # TINY
+    dm.tiny_mnk = 0.0
+    rc, out = _plan_lib([p], _cfg(0, 1), G.PATH_AUTO, dm)
+    assert out[0].route != 4

@@ -1,0 +1,119 @@
+"""Plan / execute as a hipGraph (tests/test_graph.cu T1-T3 semantics): the planned call equals
+the direct call bit for bit with equal stats, on the handle's stream and on another stream
+interleaved with direct calls, and after pointer updates there and back."""
+import ctypes as C
+
+import numpy as np
+import pytest
+import torch
+
+import ggemm as G
+from gpu_util import host, same_bits, say
+from test_gpu_grouped import CFG_AUTO, Case
+
+pytestmark = pytest.mark.gpu
+
+WORKLOADS = {
+    "tiny64": [(32, 32, 64)] * 64,
+    "moe": [(int(m), 256, 512) for m in np.random.default_rng(3).integers(16, 513, 16)],
+    "mixed": [(int(a), int(b), int(c)) for a, b, c in np.random.default_rng(4).integers(8, 385, (14, 3))]
+             + [(0, 64, 64), (48, 40, 0)],
+}
+
+
+def _problems(case, Cs, alpha, beta):
+    return [G.Problem(h.m, h.n, h.k, a.data_ptr(), h.lda, b.data_ptr(), h.ldb, c.data_ptr(), h.ldc, alpha, beta)
+            for h, a, b, c in zip(case.hp, case.dA, case.dB, Cs)]
+
+
+def _copy(dst, case):
+    for d, h in zip(dst, case.hp):
+        d.copy_(torch.from_numpy(h.C0))
+
+
+@pytest.mark.parametrize("name", sorted(WORKLOADS))
+@pytest.mark.parametrize("path", [G.PATH_EMU_GROUPED, G.PATH_AUTO])
+def test_plan_matches_direct(name, path):
+    shapes = WORKLOADS[name]
+    X = Case(shapes, 11, phi=1.0)
+    Y = Case(shapes, 22, phi=1.0)
+    cfg = CFG_AUTO if path == G.PATH_AUTO else G.Config(0, 1e-15, 0, 0)
+    hs = torch.cuda.Stream()
+    s2 = torch.cuda.Stream()
+    sizes = X.sizes()
+    h = G.Handle(len(shapes), 4 * sizes[0], 4 * sizes[1], sizes[2], stream=hs.cuda_stream)
+    mk = lambda case: [torch.empty_like(d) for d in case.dC]
+    Cref, Cg, Cref2, Cg2 = mk(X), mk(X), mk(Y), mk(Y)
+    alpha, beta = 1.5, 0.5
+    _copy(Cref, X)
+    _copy(Cg, X)
+    torch.cuda.synchronize()
+    say(f"graph T1 {name} path={path}")
+    rc, st_d = h.dgemm(path, cfg, _problems(X, Cref, alpha, beta))
+    assert rc == 0
+    arr = G.problems_array(_problems(X, Cg, alpha, beta))
+    err = C.c_int(0)
+    plan = G.lib().ggemm_make_plan_ex(h.h, path, C.byref(cfg), arr, len(shapes), C.byref(err))
+    assert plan, err.value
+    st_p = G.Stats()
+    assert G.lib().ggemm_plan_get_stats(plan, C.byref(st_p)) == 0
+    assert G.lib().ggemm_execute_plan(plan, hs.cuda_stream) == 0
+    torch.cuda.synchronize()
+    ref = np.concatenate([host(t) for t in Cref])
+    assert same_bits(np.concatenate([host(t) for t in Cg]), ref)
+    assert (st_p.num_fallback, st_p.moduli_min, st_p.moduli_max) == (st_d.num_fallback, st_d.moduli_min,
+                                                                     st_d.moduli_max)
+    assert st_p.kernel_launches == st_d.kernel_launches
+
+    say(f"graph T2 {name}")
+    py = G.problems_array(_problems(Y, Y.dC, alpha, 0.0))
+    for _ in range(4):
+        with torch.cuda.stream(s2):
+            _copy(Cg, X)
+        assert G.lib().ggemm_execute_plan(plan, s2.cuda_stream) == 0
+        st = G.Stats()
+        assert G.lib().ggemm_grouped_dgemm(h.h, path, C.byref(cfg), py, len(shapes), C.byref(st)) == 0
+    torch.cuda.synchronize()
+    assert same_bits(np.concatenate([host(t) for t in Cg]), ref)
+
+    say(f"graph T3 {name}")
+    _copy(Cref2, Y)
+    _copy(Cg2, Y)
+    torch.cuda.synchronize()
+    st = G.Stats()
+    assert G.lib().ggemm_grouped_dgemm(h.h, path, C.byref(cfg), G.problems_array(_problems(Y, Cref2, alpha, beta)),
+                                       len(shapes), C.byref(st)) == 0
+    PA = (C.c_void_p * len(shapes))(*[t.data_ptr() for t in Y.dA])
+    PB = (C.c_void_p * len(shapes))(*[t.data_ptr() for t in Y.dB])
+    PC = (C.c_void_p * len(shapes))(*[t.data_ptr() for t in Cg2])
+    assert G.lib().ggemm_plan_update_pointers(plan, PA, PB, PC) == 0
+    assert G.lib().ggemm_execute_plan(plan, s2.cuda_stream) == 0
+    torch.cuda.synchronize()
+    assert same_bits(np.concatenate([host(t) for t in Cg2]), np.concatenate([host(t) for t in Cref2]))
+    _copy(Cg, X)
+    torch.cuda.synchronize()
+    PA = (C.c_void_p * len(shapes))(*[t.data_ptr() for t in X.dA])
+    PB = (C.c_void_p * len(shapes))(*[t.data_ptr() for t in X.dB])
+    PC = (C.c_void_p * len(shapes))(*[t.data_ptr() for t in Cg])
+    assert G.lib().ggemm_plan_update_pointers(plan, PA, PB, PC) == 0
+    assert G.lib().ggemm_execute_plan(plan, hs.cuda_stream) == 0
+    torch.cuda.synchronize()
+    assert same_bits(np.concatenate([host(t) for t in Cg]), ref)
+    G.lib().ggemm_destroy_plan(plan)
+    h.close()
+
+
+def test_plan_rejects_other_paths_and_bad_pointers():
+    X = Case([(16, 16, 16)], 1, phi=0.0)
+    h = G.Handle(1, *X.sizes())
+    arr = G.problems_array(X.problems())
+    err = C.c_int(0)
+    for path in (G.PATH_NATIVE_LOOP, G.PATH_EMU_LOOP, G.PATH_EMU_LOOP_BATCHED):
+        assert not G.lib().ggemm_make_plan_ex(h.h, path, None, arr, 1, C.byref(err))
+        assert err.value == G.GGEMM_ERR_INVALID
+    plan = G.lib().ggemm_make_plan(h.h, G.PATH_AUTO, None, arr, 1)
+    assert plan
+    null = (C.c_void_p * 1)(None)
+    assert G.lib().ggemm_plan_update_pointers(plan, None, None, null) == G.GGEMM_ERR_INVALID
+    G.lib().ggemm_destroy_plan(plan)
+    h.close()

@@ -1,0 +1,313 @@
+"""End-to-end ggemm_grouped_dgemm on the GPU through the C ABI (tests/test_grouped.cu semantics).
+
+Emulated problems must equal the oracle bit for bit (same shifts, exact integer products, same
+CRT / certificate arithmetic, same sequential repair dots); native-route problems (own FP64 MFMA
+GEMM) must meet the componentwise gamma_n gate against a long-double reference.  Stats
+(num_fallback, moduli range, repair / uncertified / safety counts, launches) must equal what the
+oracle's planner and pipeline give."""
+import ctypes as C
+import os
+
+import numpy as np
+import pytest
+import torch
+
+os.environ["GGEMM_STATS_REPAIR"] = "1"   # read at handle creation
+
+import ggemm as G
+import oracle_lib as O
+from gpu_util import dev, host, same_bits, say
+
+pytestmark = pytest.mark.gpu
+
+
+def gen(rng, shape_elems, phi):
+    v = rng.random(shape_elems) - 0.5
+    if phi:
+        v *= np.exp(phi * rng.standard_normal(shape_elems))
+    return v
+
+
+class Case:
+    """A group of problems with host data (column-major, lda = m + pad) and device copies."""
+
+    def __init__(self, shapes, seed, phi=1.0, alpha=1.0, beta=0.0, pad=0):
+        rng = np.random.default_rng(seed)
+        self.hp = []
+        for s in shapes:
+            m, n, k = s[:3]
+            a = s[3] if len(s) > 3 else alpha
+            b = s[4] if len(s) > 4 else beta
+            h = O.HostProb(m, n, k, pad, phi, a, b)
+            h.ldb = max(1, k + pad)
+            h.ldc = max(1, m + pad)
+            h.lda = max(1, m + pad)
+            h.A = np.zeros(h.lda * max(k, 1))
+            h.B = np.zeros(h.ldb * max(n, 1))
+            h.C0 = np.zeros(h.ldc * max(n, 1))
+            for c in range(k):
+                h.A[c * h.lda: c * h.lda + m] = gen(rng, m, phi)
+            for c in range(n):
+                h.B[c * h.ldb: c * h.ldb + k] = gen(rng, k, phi)
+            for c in range(n):
+                h.C0[c * h.ldc: c * h.ldc + m] = gen(rng, m, 0.0)
+            self.hp.append(h)
+        self.alloc()
+
+    def alloc(self):
+        self.dA = [dev(h.A) for h in self.hp]
+        self.dB = [dev(h.B) for h in self.hp]
+        self.dC = [dev(h.C0) for h in self.hp]
+
+    def reset_C(self):
+        for d, h in zip(self.dC, self.hp):
+            d.copy_(torch.from_numpy(h.C0))
+        torch.cuda.synchronize()
+
+    def problems(self):
+        return [G.Problem(h.m, h.n, h.k, a.data_ptr(), h.lda, b.data_ptr(), h.ldb, c.data_ptr(), h.ldc, h.alpha,
+                          h.beta) for h, a, b, c in zip(self.hp, self.dA, self.dB, self.dC)]
+
+    def sizes(self):
+        return (sum(h.m * h.k for h in self.hp) + 1, sum(h.k * h.n for h in self.hp) + 1,
+                sum(h.m * h.n for h in self.hp) + 1)
+
+    def C(self, g):
+        return host(self.dC[g])
+
+
+def run(case, path, cfg, handle=None, min_k=None):
+    own = handle is None
+    if own:
+        handle = G.Handle(max(len(case.hp), 1), *case.sizes(), min_k=min_k)
+    case.reset_C()
+    rc, st = handle.dgemm(path, cfg, case.problems())
+    torch.cuda.synchronize()
+    if own:
+        handle.close()
+    return rc, st
+
+
+def oracle_plan(case, cfg, path, dm=None):
+    if dm is None:
+        dm = G.DeviceModel()
+        G.lib().ggemm_device_model_init(C.byref(dm), b"gfx950", 9, 5, 256)
+    probs = [O.Shape(h.m, h.n, h.k, h.alpha, h.beta) for h in case.hp]
+    arr = (O.Shape * max(len(probs), 1))(*probs)
+    odm = O.DeviceModel(dm.num_sms, dm.fp64_flops, dm.int8_ops, dm.mem_bw, dm.tiny_mnk)
+    out = (O.PlanEntry * max(len(probs), 1))()
+    rc = O.oracle().oz2o_plan(arr, len(probs), cfg.num_moduli, cfg.target_rel_err, cfg.allow_fallback, path,
+                              C.byref(odm), 16.0, out)
+    return rc, list(out)[:len(probs)]
+
+
+def device_model():
+    props = torch.cuda.get_device_properties(0)
+    dm = G.DeviceModel()
+    G.lib().ggemm_device_model_init(C.byref(dm), props.gcnArchName.encode(), 9, 5, props.multi_processor_count)
+    return dm
+
+
+def check_case(case, path, cfg, st, mode):
+    """Each problem vs the oracle: bitwise for emulated routes, gamma_n gate for native routes.
+    Returns the oracle's counters {uncertified, repaired, safety}."""
+    plan_path = G.PATH_EMU_LOOP if path == G.PATH_EMU_LOOP_BATCHED else path
+    rc, plan = oracle_plan(case, cfg, plan_path, device_model())
+    assert rc == 0
+    tot = np.zeros(4, dtype=np.int64)
+    nfb, nmin, nmax = 0, 99, 0
+    for g, (h, e) in enumerate(zip(case.hp, plan)):
+        Cg = case.C(g)
+        if e.route == 1:   # EMPTY: C untouched
+            assert same_bits(Cg, h.C0), g
+            continue
+        if e.route == 0:
+            nmin, nmax = min(nmin, e.num_moduli), max(nmax, e.num_moduli)
+            Co, cnt = h.emulate(mode, e.num_moduli)
+            tot += cnt
+            assert same_bits(Cg, Co), f"problem {g} ({h.m}x{h.n}x{h.k}) differs"
+        else:
+            nfb += O.oracle().oz2o_route_is_fallback(e.route)
+            h.reference()
+            gate, over = h.gate(Cg)
+            if np.isfinite(h.A).all() and np.isfinite(h.B).all() and np.isfinite(h.C0).all():
+                assert gate <= 1.0, f"native problem {g} gate {gate}"
+    assert st.num_fallback == nfb
+    if nmax:
+        assert (st.moduli_min, st.moduli_max) == (nmin, nmax)
+    assert (st.num_uncertified, st.num_repaired, st.num_safety_fallback) == (tot[1], tot[2], tot[3])
+    return tot
+
+
+CFG_EMU = G.Config(0, 1e-15, 0, 0)
+CFG_AUTO = G.Config(0, 1e-15, 1, 0)
+
+
+def test_config1_plumbing_fixed_n14():
+    """G=1, 256^3, U(-0.5,0.5), alpha=1 beta=0, fixed N=14 (EMU_GROUPED, COUNT mode)."""
+    case = Case([(256, 256, 256)], 20261201, phi=0.0)
+    say("config1 256^3 N=14")
+    cfg = G.Config(14, 1e-15, 1, 0)
+    rc, st = run(case, G.PATH_EMU_GROUPED, cfg)
+    assert rc == 0
+    assert st.kernel_launches == 3 and st.moduli_min == st.moduli_max == 14 and st.num_fallback == 0
+    check_case(case, G.PATH_EMU_GROUPED, cfg, st, O.REPAIR_COUNT)
+
+
+@pytest.mark.parametrize("path", [G.PATH_EMU_GROUPED, G.PATH_AUTO, G.PATH_EMU_LOOP, G.PATH_EMU_LOOP_BATCHED])
+def test_uniform_group_beta(path):
+    """Config-2 shape family, reduced: G=8 x 192^3, (U-0.5)exp(0.5 Z), alpha=1, beta=0.5."""
+    case = Case([(192, 192, 192)] * 8, 20261202, phi=0.5, beta=0.5)
+    cfg = CFG_AUTO if path == G.PATH_AUTO else CFG_EMU
+    say(f"uniform group path={path}")
+    rc, st = run(case, path, cfg)
+    assert rc == 0
+    check_case(case, path, cfg, st, O.REPAIR_ON if path == G.PATH_AUTO else O.REPAIR_COUNT)
+    if path in (G.PATH_EMU_GROUPED, G.PATH_AUTO):
+        assert st.kernel_launches == 3
+
+
+def test_ragged_group_auto():
+    """Config-3 family, reduced: m, n log-uniform in [16, 300], k log-uniform in [1, 700] (k <= 16
+    takes SMALL_K, k in (16, 32) exercises Kp padding), alpha ~ U(-2, 2) with 3 zeros,
+    beta ~ U(-1, 1), phi = 1, AUTO with create_ex(min_k = 1)."""
+    rng = np.random.default_rng(20261203)
+    shapes = []
+    for g in range(24):
+        m, n = (int(np.exp(rng.uniform(np.log(16), np.log(300)))) for _ in range(2))
+        k = int(np.exp(rng.uniform(0, np.log(700))))
+        a = 0.0 if g in (3, 11, 19) else float(rng.uniform(-2, 2))
+        shapes.append((m, n, k, a, float(rng.uniform(-1, 1))))
+    shapes[5] = (40, 33, 20, 1.0, 0.0)   # k in (16, 32)
+    case = Case(shapes, 7, phi=1.0)
+    say("ragged auto")
+    rc, st = run(case, G.PATH_AUTO, CFG_AUTO, min_k=1)
+    assert rc == 0
+    check_case(case, G.PATH_AUTO, CFG_AUTO, st, O.REPAIR_ON)
+
+
+def test_hard_numerics_nan_inf_and_repair():
+    """Config-5 family, reduced: (U-0.5)exp(4Z), 0.1% NaN/Inf entries, repair ON (AUTO)."""
+    case = Case([(96, 80, 256)] * 4 + [(64, 64, 3000)], 20261205, phi=4.0)
+    rng = np.random.default_rng(5)
+    for h in case.hp:
+        for arr, rows, cols, ld in ((h.A, h.m, h.k, h.lda), (h.B, h.k, h.n, h.ldb)):
+            nbad = max(1, rows * cols // 1000)
+            r = rng.integers(0, rows, nbad)
+            c = rng.integers(0, cols, nbad)
+            arr[r + c * ld] = rng.choice([np.nan, np.inf, -np.inf], nbad)
+    case.alloc()
+    say("hard numerics")
+    rc, st = run(case, G.PATH_AUTO, CFG_AUTO)
+    assert rc == 0
+    tot = check_case(case, G.PATH_AUTO, CFG_AUTO, st, O.REPAIR_ON)
+    assert tot[3] > 0
+
+
+def test_edge_cases():
+    say("edge: num_problems = 0")
+    with G.Handle(4, 64, 64, 64) as h:
+        for path in range(7):
+            st = G.Stats()
+            rc = G.lib().ggemm_grouped_dgemm(h.h, path, C.byref(CFG_EMU), None, 0, C.byref(st))
+            assert rc == (G.GGEMM_ERR_INVALID if path == G.PATH_EMU_GROUPED_REUSE else 0), path
+            if rc == 0:
+                assert st.num_problems == 0 and st.num_fallback == 0
+    cases = [([(100, 70, 50)], 1.0, 0.0), ([(1, 1, 1)], 1.0, 0.0),
+             ([(0, 32, 32), (32, 0, 32), (32, 32, 0), (48, 40, 36), (0, 0, 0)], 1.5, -0.5),
+             ([(0, 16, 16), (16, 0, 16)], 1.0, 0.0), ([(33, 31, 1), (65, 3, 31), (5, 129, 97)], -2.0, 1.0)]
+    for shapes, a, b in cases:
+        case = Case(shapes, 12345 + len(shapes), phi=1.0, alpha=a, beta=b)
+        for path, cfg, mode in [(G.PATH_EMU_GROUPED, CFG_EMU, O.REPAIR_COUNT), (G.PATH_AUTO, CFG_AUTO, O.REPAIR_ON)]:
+            say(f"edge {shapes} path={path}")
+            rc, st = run(case, path, cfg, min_k=1)
+            assert rc == 0
+            check_case(case, path, cfg, st, mode)
+    # beta = 0 must not read C: NaN-filled C0
+    case = Case([(40, 24, 72), (17, 33, 5)], 99, phi=1.0)
+    for h in case.hp:
+        h.C0[:] = np.nan
+    case.alloc()
+    say("edge beta0 NaN C")
+    rc, st = run(case, G.PATH_EMU_GROUPED, CFG_EMU, min_k=1)
+    assert rc == 0
+    for g in range(2):
+        assert np.isfinite(case.C(g).reshape(case.hp[g].n, case.hp[g].ldc)[:, :case.hp[g].m]).all()
+
+
+@pytest.mark.parametrize("path", [G.PATH_NATIVE_LOOP, G.PATH_NATIVE_GROUPED])
+def test_native_paths_gate(path):
+    case = Case([(100, 70, 50), (64, 64, 300), (1, 1, 1), (33, 17, 0), (0, 5, 5)], 31, phi=1.0, alpha=1.5, beta=-0.5)
+    say(f"native path {path}")
+    rc, st = run(case, path, CFG_EMU)
+    assert rc == 0
+    for g, h in enumerate(case.hp):
+        if h.m == 0 or h.n == 0:
+            continue
+        h.reference()
+        gate, _ = h.gate(case.C(g))
+        assert gate <= 1.0, (g, gate)
+    assert st.kernel_launches == (1 if path == G.PATH_NATIVE_GROUPED else 4)
+
+
+def test_bigk_fallback_and_unsafe():
+    """k = 140000 > 131040: AUTO with fallback -> native route counted; allow_fallback = 0 ->
+    GGEMM_ERR_UNSAFE (tests/test_grouped.cu:185-231)."""
+    case = Case([(4, 4, 140000), (64, 64, 64), (8, 8, 8)], 5, phi=0.5)
+    say("bigk fallback")
+    rc, st = run(case, G.PATH_AUTO, CFG_AUTO)
+    assert rc == 0 and st.num_fallback >= 1
+    check_case(case, G.PATH_AUTO, CFG_AUTO, st, O.REPAIR_ON)
+    for path in (G.PATH_EMU_GROUPED, G.PATH_AUTO):
+        rc, st = run(case, path, G.Config(0, 1e-15, 0, 0))
+        assert rc == G.GGEMM_ERR_UNSAFE
+
+
+def test_capacity_and_argument_errors():
+    case = Case([(16, 16, 16)] * 3, 3, phi=0.0)
+    say("capacity errors")
+    for path in (G.PATH_NATIVE_LOOP, G.PATH_NATIVE_GROUPED, G.PATH_EMU_LOOP, G.PATH_EMU_GROUPED, G.PATH_AUTO):
+        with G.Handle(2, 4096, 4096, 4096) as h:
+            rc, _ = h.dgemm(path, CFG_AUTO, case.problems())
+            assert rc == G.GGEMM_ERR_INVALID
+        with G.Handle(8, 100, 100, 100) as h:
+            rc, _ = h.dgemm(path, CFG_AUTO, case.problems())
+            assert rc == G.GGEMM_ERR_WORKSPACE
+    with G.Handle(8, 4096, 4096, 4096) as h:
+        for path in (G.PATH_EMU_GROUPED, G.PATH_AUTO):
+            for bad in (1, G.MAX_MODULI + 1, -1):
+                rc, _ = h.dgemm(path, G.Config(bad, 1e-15, 1, 0), case.problems())
+                assert rc == G.GGEMM_ERR_INVALID
+            rc, _ = h.dgemm(path, G.Config(0, 1e-15, 1, 7), case.problems())   # repair mode out of range
+            assert rc == G.GGEMM_ERR_INVALID
+    # k < min_k residue inflation -> WORKSPACE with one diagnostic line
+    small = Case([(64, 64, 1)] * 2, 4, phi=0.0)
+    with G.Handle(2, 64 * 2, 64 * 2, 64 * 64 * 2) as h:
+        rc, _ = h.dgemm(G.PATH_EMU_GROUPED, CFG_EMU, small.problems())
+        assert rc == G.GGEMM_ERR_WORKSPACE
+    torch.cuda.synchronize()
+
+
+def test_launch_count_independent_of_group_size():
+    launches = []
+    for n_probs in (16, 1024):
+        case = Case([(32, 32, 32)] * n_probs, 8, phi=0.5)
+        say(f"launch count G={n_probs}")
+        rc, st = run(case, G.PATH_EMU_GROUPED, CFG_EMU)
+        assert rc == 0
+        launches.append(st.kernel_launches)
+    assert launches[0] == launches[1] == 3
+
+
+@pytest.mark.parametrize("path", [G.PATH_EMU_GROUPED, G.PATH_AUTO, G.PATH_NATIVE_GROUPED])
+def test_bitwise_reproducible(path):
+    case = Case([(int(m), 256, 512) for m in np.random.default_rng(2).integers(16, 513, 12)], 9, phi=1.0)
+    say(f"reproducibility path={path}")
+    with G.Handle(len(case.hp), *case.sizes()) as h:
+        outs = []
+        for _ in range(2):
+            case.reset_C()
+            rc, _ = h.dgemm(path, CFG_AUTO if path == G.PATH_AUTO else CFG_EMU, case.problems())
+            assert rc == 0
+            outs.append(np.concatenate([case.C(g) for g in range(len(case.hp))]))
+        assert same_bits(outs[0], outs[1])
