@@ -97,18 +97,19 @@ __global__ void __launch_bounds__(kThreads) f64_grouped_kernel(const F64Problem*
       __syncthreads();
     }
   }
-  // D block layout: lane l, register r -> row 4 (l / 16) + r, column l % 16
+  // D block layout of v_mfma_f64_16x16x4f64: lane l, register r -> row 4 r + l / 16, column l % 16
+  // (four single-row groups; the INT8 / F32 16 x 16 instructions use four consecutive rows instead)
   const size_t ldc = (size_t)P.ldc;
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int col = col0 + wn * 32 + j * 16 + (lane & 15);
-      const int rbase = row0 + wm * 32 + i * 16 + 4 * (lane >> 4);
+      const int rbase = row0 + wm * 32 + i * 16 + (lane >> 4);
       if (col >= P.n) continue;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int row = rbase + r;
+        const int row = rbase + 4 * r;
         if (row >= P.m) continue;
         double* cp = P.C + (size_t)row + (size_t)col * ldc;
         const double ab = compute ? P.alpha * acc[i][j][r] : 0.0;

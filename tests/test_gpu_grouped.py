@@ -133,6 +133,15 @@ def check_case(case, path, cfg, st, mode):
             if np.isfinite(h.A).all() and np.isfinite(h.B).all() and np.isfinite(h.C0).all():
                 assert gate <= 1.0, f"native problem {g} gate {gate}"
     assert st.num_fallback == nfb
+    n_emu = sum(1 for e in plan if e.route == 0)
+    n_nat = sum(1 for e in plan if e.route not in (0, 1))
+    if path in (G.PATH_EMU_GROUPED, G.PATH_AUTO):
+        want = (3 if n_emu else 0) + (1 if n_nat else 0)
+    elif path == G.PATH_EMU_LOOP:
+        want = sum(e.num_moduli + 3 for e in plan if e.route == 0) + (1 if n_nat else 0)
+    else:
+        want = 3 * n_emu + (1 if n_nat else 0)
+    assert st.kernel_launches == want, (st.kernel_launches, want)
     if nmax:
         assert (st.moduli_min, st.moduli_max) == (nmin, nmax)
     assert (st.num_uncertified, st.num_repaired, st.num_safety_fallback) == (tot[1], tot[2], tot[3])
@@ -163,8 +172,6 @@ def test_uniform_group_beta(path):
     rc, st = run(case, path, cfg)
     assert rc == 0
     check_case(case, path, cfg, st, O.REPAIR_ON if path == G.PATH_AUTO else O.REPAIR_COUNT)
-    if path in (G.PATH_EMU_GROUPED, G.PATH_AUTO):
-        assert st.kernel_launches == 3
 
 
 def test_ragged_group_auto():
@@ -197,11 +204,16 @@ def test_hard_numerics_nan_inf_and_repair():
             c = rng.integers(0, cols, nbad)
             arr[r + c * ld] = rng.choice([np.nan, np.inf, -np.inf], nbad)
     case.alloc()
-    say("hard numerics")
+    say("hard numerics EMU_GROUPED repair ON")
+    cfg = G.Config(0, 1e-15, 1, G.REPAIR_ON)
+    rc, st = run(case, G.PATH_EMU_GROUPED, cfg)
+    assert rc == 0
+    tot = check_case(case, G.PATH_EMU_GROUPED, cfg, st, O.REPAIR_ON)
+    assert tot[3] > 0 and tot[2] > 0
+    say("hard numerics AUTO")
     rc, st = run(case, G.PATH_AUTO, CFG_AUTO)
     assert rc == 0
-    tot = check_case(case, G.PATH_AUTO, CFG_AUTO, st, O.REPAIR_ON)
-    assert tot[3] > 0
+    check_case(case, G.PATH_AUTO, CFG_AUTO, st, O.REPAIR_ON)
 
 
 def test_edge_cases():
