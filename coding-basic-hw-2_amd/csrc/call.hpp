@@ -5,10 +5,11 @@
 namespace ggemm {
 
 // Descriptor blob (identical in the pinned host mirror and the device copy):
-//   [oz2_problem x ne][i8_problem x n_i8][F64Problem x nn][F64 schedule(s)][INT8 schedule(s)]
+//   [oz2_problem x ne][YDesc x ne][i8_problem x n_i8][I8Epi x n_i8][F64Problem x nn]
+//   [F64 schedule(s)][INT8 schedule(s)]
 // every section 256-byte aligned; the INT8 schedule is last so the H2D can stop at its used size.
 struct BlobLayout {
-  size_t off_oz, off_i8, off_f64, off_sf64, off_si8, total;
+  size_t off_oz, off_yd, off_i8, off_epi, off_f64, off_sf64, off_si8, total;
 };
 BlobLayout layout_for(size_t ne, size_t n_i8, size_t nn, size_t sched_f64, size_t sched_i8);
 inline size_t sched_img(int entries) { return align_up(sched_bytes(entries), kBufAlign); }

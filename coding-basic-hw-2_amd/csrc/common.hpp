@@ -71,11 +71,26 @@ inline size_t sched_bytes(int entries) {
 
 // INT8 GEMM tile configurations (edge of the square output tile).
 constexpr int kI8NumCfg = 3;
-inline int i8_tile_edge(int cfg) { return cfg == 0 ? 128 : (cfg == 1 ? 64 : 32); }
+inline int i8_tile_edge(int cfg) { return cfg == 0 ? 256 : (cfg == 1 ? 128 : 64); }
+// Per-product epilogue of the INT8 GEMM: mode 0 stores the int32 product (C is int32*, ld m);
+// mode 1 stores the CRT digit y = ((C mod p) q) mod p as one byte (C is uint8_t*, ld m).
+struct I8Epi {
+  uint32_t mode, p, magic, q;
+};
 // Builds the INT8 schedule (LPT order); cfg < 0 in a problem selects automatically.
 int i8_build_schedule(const i8_problem* h, int num, void* h_ws, size_t ws_bytes, i8_sched_info* info,
                       int num_cus);
-int i8_launch(const i8_problem* d_probs, const void* d_sched, const i8_sched_info* info, hipStream_t s);
+// d_epi: per-problem epilogues in device memory, or nullptr for int32 products everywhere.
+int i8_launch(const i8_problem* d_probs, const I8Epi* d_epi, const void* d_sched, const i8_sched_info* info,
+              hipStream_t s);
+
+// Where the reconstruct reads a problem's plane products in the production pipeline: CRT digits
+// y_l (one byte per entry, plane l at Y + l * y_stride, ld m) and the abs-plane product L (int32).
+struct YDesc {
+  const uint8_t* Y;
+  size_t y_stride;
+  const int32_t* L;
+};
 
 // FP64 MFMA grouped GEMM (native routes).  h_ws receives the schedule image.
 int f64_build_schedule(const F64Problem* h, int num, void* h_ws, size_t ws_bytes, int* total_tiles,
@@ -84,7 +99,8 @@ int f64_launch(const F64Problem* d_probs, const void* d_sched, int total_tiles, 
 
 // Launchers used by the orchestration (return 0 on success).
 int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t s);
-int recon_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t s, int mode);
+// yd == nullptr: read the int32 planes of oz2_problem::C32 (kernel-level API); else the digits.
+int recon_launch(const oz2_problem* d, const YDesc* yd, int num, int max_m, int max_n, hipStream_t s, int mode);
 
 }  // namespace ggemm
 

@@ -58,8 +58,10 @@ void mark(int s, int q, hipStream_t st) {
 BlobLayout layout_for(size_t ne, size_t n_i8, size_t nn, size_t sched_f64, size_t sched_i8) {
   BlobLayout L;
   L.off_oz = 0;
-  L.off_i8 = align_up(ne * sizeof(oz2_problem), kBufAlign);
-  L.off_f64 = align_up(L.off_i8 + n_i8 * sizeof(i8_problem), kBufAlign);
+  L.off_yd = align_up(ne * sizeof(oz2_problem), kBufAlign);
+  L.off_i8 = align_up(L.off_yd + ne * sizeof(YDesc), kBufAlign);
+  L.off_epi = align_up(L.off_i8 + n_i8 * sizeof(i8_problem), kBufAlign);
+  L.off_f64 = align_up(L.off_epi + n_i8 * sizeof(I8Epi), kBufAlign);
   L.off_sf64 = align_up(L.off_f64 + nn * sizeof(F64Problem), kBufAlign);
   L.off_si8 = align_up(L.off_sf64 + sched_f64, kBufAlign);
   L.total = L.off_si8 + sched_i8;
@@ -172,9 +174,18 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
   c.L = layout_for(c.ne, c.n_i8, c.nn, s_f64, s_i8);
   if (c.L.total > cap) return GGEMM_ERR_INVALID;
   oz2_problem* hoz = reinterpret_cast<oz2_problem*>(hb + c.L.off_oz);
+  YDesc* hyd = reinterpret_cast<YDesc*>(hb + c.L.off_yd);
   i8_problem* hi8 = reinterpret_cast<i8_problem*>(hb + c.L.off_i8);
+  I8Epi* hepi = reinterpret_cast<I8Epi*>(hb + c.L.off_epi);
   F64Problem* hf = reinterpret_cast<F64Problem*>(hb + c.L.off_f64);
-  size_t oa = 0, ob = 0, oc = 0, orow = 0, ocol = 0, q = 0;
+  const CrtTables* tab = host_tables();
+  // product workspace (the C32 buffer): CRT digit planes [plane < nmax][problem] of SY bytes
+  // each, then the int32 abs-plane products; fits because nmax SY + 4 SC <= pmax 4 SC.
+  size_t SY = 0;
+  for (int j = 0; j < c.ne; ++j) SY += align_up((size_t)probs[emu_idx[j]].m * probs[emu_idx[j]].n, kBufAlign);
+  uint8_t* ybase = reinterpret_cast<uint8_t*>(h->C32);
+  int32_t* lbase = reinterpret_cast<int32_t*>(ybase + (size_t)nmax * SY);
+  size_t oa = 0, ob = 0, oc = 0, orow = 0, ocol = 0, q = 0, oy = 0, ol = 0;
   for (int j = 0; j < c.ne; ++j) {
     const int g = emu_idx[j];
     const ggemm_problem_t& p = probs[g];
@@ -186,15 +197,28 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
     o.A = p.A; o.B = p.B; o.C = p.C; o.alpha = p.alpha; o.beta = p.beta;
     o.A8 = h->A8 + oa; o.a8_mod_stride = SA;
     o.B8 = h->B8 + ob; o.b8_mod_stride = SB;
-    o.C32 = h->C32 + oc; o.c32_mod_stride = SC;
     o.row_shift = h->row_shift + orow; o.col_shift = h->col_shift + ocol;
-    const int planes = e.num_moduli + OZ2_EXTRA_PLANES;
-    for (int l = 0; l < planes; ++l, ++q) {
+    YDesc& yd = hyd[j];
+    yd.Y = ybase + oy;
+    yd.y_stride = SY;
+    yd.L = lbase + ol;
+    o.C32 = lbase + ol; o.c32_mod_stride = 0;   // the reconstruct reads yd, not C32
+    const int N = e.num_moduli;
+    for (int l = 0; l <= N; ++l, ++q) {
       i8_problem& d = hi8[q];
       d.m = p.m; d.n = p.n; d.kp = (int)kp;
-      d.A = o.A8 + (size_t)l * SA; d.B = o.B8 + (size_t)l * SB; d.C = o.C32 + (size_t)l * SC;
+      d.A = o.A8 + (size_t)l * SA; d.B = o.B8 + (size_t)l * SB;
       d.tile_cfg = -1;
+      if (l < N) {
+        d.C = reinterpret_cast<int32_t*>(ybase + oy + (size_t)l * SY);
+        hepi[q] = I8Epi{1u, (uint32_t)tab->p[l], tab->magic[l], (uint32_t)tab->qinv[N][l]};
+      } else {
+        d.C = lbase + ol;
+        hepi[q] = I8Epi{0u, 1u, 0u, 0u};
+      }
     }
+    oy += align_up((size_t)p.m * p.n, kBufAlign);
+    ol += align_up((size_t)p.m * p.n, kBufAlign / 4);
     oa += align_up((size_t)p.m * kp, kBufAlign);
     ob += align_up((size_t)p.n * kp, kBufAlign);
     oc += align_up((size_t)p.m * p.n, kBufAlign / 4);
@@ -214,16 +238,18 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
 
 int enqueue_grouped(const GroupedCall& c, const char* db, hipStream_t s, int repair, int* launches, int prof_set) {
   const oz2_problem* doz = reinterpret_cast<const oz2_problem*>(db + c.L.off_oz);
+  const YDesc* dyd = reinterpret_cast<const YDesc*>(db + c.L.off_yd);
   prof::mark(prof_set, 0, s);
   if (c.ne > 0) {
     if (prep_launch(doz, c.ne, c.max_m, c.max_n, s)) return GGEMM_ERR_NUMERICS;
     ++*launches;
     prof::mark(prof_set, 1, s);
-    if (i8_launch(reinterpret_cast<const i8_problem*>(db + c.L.off_i8), db + c.L.off_si8, &c.i8info, s))
+    if (i8_launch(reinterpret_cast<const i8_problem*>(db + c.L.off_i8), reinterpret_cast<const I8Epi*>(db + c.L.off_epi),
+                  db + c.L.off_si8, &c.i8info, s))
       return GGEMM_ERR_I8GEMM;
     *launches += c.i8info.num_launches;
     prof::mark(prof_set, 2, s);
-    if (recon_launch(doz, c.ne, c.max_m, c.max_n, s, repair)) return GGEMM_ERR_NUMERICS;
+    if (recon_launch(doz, dyd, c.ne, c.max_m, c.max_n, s, repair)) return GGEMM_ERR_NUMERICS;
     ++*launches;
     prof::mark(prof_set, 3, s);
   } else {
@@ -346,24 +372,27 @@ int path_emu_loop(ggemm_handle_t h, bool batched, const ggemm_problem_t* probs, 
   if (!r && hipMemcpyAsync(db, hb, base + nimg * per, hipMemcpyHostToDevice, h->stream) != hipSuccess) r = GGEMM_ERR_CUDA;
   int& nl = st->kernel_launches;
   const oz2_problem* doz = reinterpret_cast<const oz2_problem*>(db + c.L.off_oz);
+  const YDesc* dyd = reinterpret_cast<const YDesc*>(db + c.L.off_yd);
   const i8_problem* di8 = reinterpret_cast<const i8_problem*>(db + c.L.off_i8);
+  const I8Epi* depi = reinterpret_cast<const I8Epi*>(db + c.L.off_epi);
   q = 0;
   for (int j = 0; j < c.ne && !r; ++j) {
     const int planes = hoz[j].num_moduli + OZ2_EXTRA_PLANES;
     if (prep_launch(doz + j, 1, hoz[j].m, hoz[j].n, h->stream)) { r = GGEMM_ERR_NUMERICS; break; }
     ++nl;
     if (batched) {
-      if (i8_launch(di8 + q, db + base + j * per, &h->loop_info[j], h->stream)) { r = GGEMM_ERR_I8GEMM; break; }
+      if (i8_launch(di8 + q, depi + q, db + base + j * per, &h->loop_info[j], h->stream)) { r = GGEMM_ERR_I8GEMM; break; }
       nl += h->loop_info[j].num_launches;
     } else {
       for (int l = 0; l < planes && !r; ++l) {
-        if (i8_launch(di8 + q + l, db + base + (q + l) * per, &h->loop_info[q + l], h->stream)) r = GGEMM_ERR_I8GEMM;
+        if (i8_launch(di8 + q + l, depi + q + l, db + base + (q + l) * per, &h->loop_info[q + l], h->stream))
+          r = GGEMM_ERR_I8GEMM;
         else nl += h->loop_info[q + l].num_launches;
       }
       if (r) break;
     }
     q += planes;
-    if (recon_launch(doz + j, 1, hoz[j].m, hoz[j].n, h->stream, repair)) { r = GGEMM_ERR_NUMERICS; break; }
+    if (recon_launch(doz + j, dyd + j, 1, hoz[j].m, hoz[j].n, h->stream, repair)) { r = GGEMM_ERR_NUMERICS; break; }
     ++nl;
   }
   if (!r && c.nn > 0 && c.f64_tiles > 0) {

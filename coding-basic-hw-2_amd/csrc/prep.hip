@@ -152,11 +152,15 @@ __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ t
   double mx = 0.0, ss = 0.0;
   if (valid) {
     int k = c;
-    for (; k + 24 < K; k += 32) {
-      const double a0 = A[i + (size_t)k * lda], a1 = A[i + (size_t)(k + 8) * lda];
-      const double a2 = A[i + (size_t)(k + 16) * lda], a3 = A[i + (size_t)(k + 24) * lda];
-      mx = fmax(fmax(fmax(fmax(mx, fabs(a0)), fabs(a1)), fabs(a2)), fabs(a3));
-      ss = fma(a0, a0, ss); ss = fma(a1, a1, ss); ss = fma(a2, a2, ss); ss = fma(a3, a3, ss);
+    for (; k + 8 * 15 < K; k += 8 * 16) {   // 16 loads in flight, then the ordered chain
+      double a[16];
+#pragma unroll
+      for (int t = 0; t < 16; ++t) a[t] = A[i + (size_t)(k + 8 * t) * lda];
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {
+        mx = fmax(mx, fabs(a[t]));
+        ss = fma(a[t], a[t], ss);
+      }
     }
     for (; k < K; k += 8) {
       const double a = A[i + (size_t)k * lda];
@@ -214,11 +218,16 @@ __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ t
   const int l0 = split == 0 ? 0 : w0, l1 = split == 0 ? ntile : w1;   // tiles walked here
   for (int t = l0; t < l1; ++t) {
     const int k0 = t * kATile;
-#pragma unroll 4
+    double av[kATile / kChains];
+#pragma unroll
+    for (int jj = 0; jj < kATile / kChains; ++jj) {
+      const int k = k0 + c + kChains * jj;
+      av[jj] = (valid && k < K) ? A[i + (size_t)k * lda] : 0.0;
+    }
+#pragma unroll
     for (int jj = 0; jj < kATile / kChains; ++jj) {
       const int kk = c + kChains * jj;
-      const int k = k0 + kk;
-      const double a = (valid && k < K) ? A[i + (size_t)k * lda] : 0.0;
+      const double a = av[jj];
       if (!nf_c && split == 0) {
         const double xs = mul_pow2(a, sh_c);
         const double xt = trunc(xs);
@@ -286,7 +295,18 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
   const double T = tab->T[N];
 
   double mx = 0.0, ss = 0.0;
-  for (int k = lane; k < K; k += 32) {
+  int k = lane;
+  for (; k + 32 * 7 < K; k += 32 * 8) {   // 8 loads in flight, then the ordered chain
+    double a[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) a[t] = b[k + 32 * t];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      mx = fmax(mx, fabs(a[t]));
+      ss = fma(a[t], a[t], ss);
+    }
+  }
+  for (; k < K; k += 32) {
     const double a = b[k];
     mx = fmax(mx, fabs(a));
     ss = fma(a, a, ss);
