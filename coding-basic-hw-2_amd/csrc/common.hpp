@@ -69,14 +69,23 @@ inline size_t sched_bytes(int entries) {
   return sizeof(int) * (size_t)(kSchedHdr + 2 * (size_t)entries + 1 + 8);
 }
 
-// INT8 GEMM tile configurations (edge of the square output tile).
+// INT8 GEMM tile configurations (output tile rows x columns).
 constexpr int kI8NumCfg = 3;
-inline int i8_tile_edge(int cfg) { return cfg == 0 ? 256 : (cfg == 1 ? 128 : 64); }
+__host__ __device__ inline int i8_tile_m(int cfg) { return cfg == 0 ? 256 : (cfg == 1 ? 128 : 64); }
+__host__ __device__ inline int i8_tile_n(int cfg) { return cfg == 0 ? 128 : (cfg == 1 ? 128 : 64); }
 // Per-product epilogue of the INT8 GEMM: mode 0 stores the int32 product (C is int32*, ld m);
-// mode 1 stores the CRT digit y = ((C mod p) q) mod p as one byte (C is uint8_t*, ld m).
+// mode 1 stores one byte per entry, the residue C mod p in [0, p), computed as
+// u = C + bias (bias = p ceil(2^31 / p), so 0 <= u < 2^32), u - p umulhi(u, mc) (mc = ceil(2^32 / p)),
+// plus p when that is negative.  In the production pipeline the A residues of plane l carry the
+// CRT inverse q_l (prep with fold_q), so this byte is the CRT digit y_l = (C_l q_l) mod p_l.
 struct I8Epi {
-  uint32_t mode, p, magic, q;
+  uint32_t mode, p, mc, bias;
 };
+inline I8Epi i8_epi_residue(uint32_t p) {
+  const uint32_t mc = (uint32_t)((4294967296ull + p - 1) / p);
+  const uint32_t bias = p * (uint32_t)((2147483648ull + p - 1) / p);
+  return I8Epi{1u, p, mc, bias};
+}
 // Builds the INT8 schedule (LPT order); cfg < 0 in a problem selects automatically.
 int i8_build_schedule(const i8_problem* h, int num, void* h_ws, size_t ws_bytes, i8_sched_info* info,
                       int num_cus);
@@ -98,7 +107,9 @@ int f64_build_schedule(const F64Problem* h, int num, void* h_ws, size_t ws_bytes
 int f64_launch(const F64Problem* d_probs, const void* d_sched, int total_tiles, hipStream_t s);
 
 // Launchers used by the orchestration (return 0 on success).
-int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t s);
+// fold_q != 0: the residues of A plane l are (q_l r) mod p_l (symmetric) instead of r, with q_l the
+// CRT inverse of modulus l for the problem's N; the abs plane and B are unchanged.
+int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t s, int fold_q = 0);
 // yd == nullptr: read the int32 planes of oz2_problem::C32 (kernel-level API); else the digits.
 int recon_launch(const oz2_problem* d, const YDesc* yd, int num, int max_m, int max_n, hipStream_t s, int mode);
 

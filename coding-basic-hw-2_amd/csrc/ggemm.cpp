@@ -185,7 +185,7 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
   for (int j = 0; j < c.ne; ++j) SY += align_up((size_t)probs[emu_idx[j]].m * probs[emu_idx[j]].n, kBufAlign);
   uint8_t* ybase = reinterpret_cast<uint8_t*>(h->C32);
   int32_t* lbase = reinterpret_cast<int32_t*>(ybase + (size_t)nmax * SY);
-  size_t oa = 0, ob = 0, oc = 0, orow = 0, ocol = 0, q = 0, oy = 0, ol = 0;
+  size_t oa = 0, ob = 0, orow = 0, ocol = 0, q = 0, oy = 0, ol = 0;
   for (int j = 0; j < c.ne; ++j) {
     const int g = emu_idx[j];
     const ggemm_problem_t& p = probs[g];
@@ -211,7 +211,7 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
       d.tile_cfg = -1;
       if (l < N) {
         d.C = reinterpret_cast<int32_t*>(ybase + oy + (size_t)l * SY);
-        hepi[q] = I8Epi{1u, (uint32_t)tab->p[l], tab->magic[l], (uint32_t)tab->qinv[N][l]};
+        hepi[q] = i8_epi_residue((uint32_t)tab->p[l]);   // A residues carry q_l: the byte is y_l
       } else {
         d.C = lbase + ol;
         hepi[q] = I8Epi{0u, 1u, 0u, 0u};
@@ -221,7 +221,6 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
     ol += align_up((size_t)p.m * p.n, kBufAlign / 4);
     oa += align_up((size_t)p.m * kp, kBufAlign);
     ob += align_up((size_t)p.n * kp, kBufAlign);
-    oc += align_up((size_t)p.m * p.n, kBufAlign / 4);
     orow += align_up((size_t)OZ2_ROW_WS_PER_ROW * p.m, 64);
     ocol += align_up((size_t)OZ2_ROW_WS_PER_ROW * p.n, 64);
     c.max_m = std::max(c.max_m, p.m);
@@ -241,7 +240,7 @@ int enqueue_grouped(const GroupedCall& c, const char* db, hipStream_t s, int rep
   const YDesc* dyd = reinterpret_cast<const YDesc*>(db + c.L.off_yd);
   prof::mark(prof_set, 0, s);
   if (c.ne > 0) {
-    if (prep_launch(doz, c.ne, c.max_m, c.max_n, s)) return GGEMM_ERR_NUMERICS;
+    if (prep_launch(doz, c.ne, c.max_m, c.max_n, s, 1)) return GGEMM_ERR_NUMERICS;
     ++*launches;
     prof::mark(prof_set, 1, s);
     if (i8_launch(reinterpret_cast<const i8_problem*>(db + c.L.off_i8), reinterpret_cast<const I8Epi*>(db + c.L.off_epi),
@@ -378,7 +377,7 @@ int path_emu_loop(ggemm_handle_t h, bool batched, const ggemm_problem_t* probs, 
   q = 0;
   for (int j = 0; j < c.ne && !r; ++j) {
     const int planes = hoz[j].num_moduli + OZ2_EXTRA_PLANES;
-    if (prep_launch(doz + j, 1, hoz[j].m, hoz[j].n, h->stream)) { r = GGEMM_ERR_NUMERICS; break; }
+    if (prep_launch(doz + j, 1, hoz[j].m, hoz[j].n, h->stream, 1)) { r = GGEMM_ERR_NUMERICS; break; }
     ++nl;
     if (batched) {
       if (i8_launch(di8 + q, depi + q, db + base + j * per, &h->loop_info[j], h->stream)) { r = GGEMM_ERR_I8GEMM; break; }

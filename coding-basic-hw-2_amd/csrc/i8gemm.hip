@@ -9,22 +9,27 @@
 //   * XCD-aware dispatch: MI355X deals workgroups round-robin to its 8 XCDs (b mod 8), each with
 //     its own L2.  Workgroup b is mapped to tile chunk (b mod 8) + 8 (b / (8 C)) of C = 32
 //     consecutive table tiles, so one XCD works through contiguous runs of the table;
-//   * inside an entry tiles are rastered in groups of 8 tile-rows (8 x 4 blocks of 32 tiles),
-//     so the 32 compute units of an XCD share 8 A panels and 4 B panels.
-// Tile configurations, 512 threads = 8 waves in a 2 (M) x 4 (N) arrangement:
-//   cfg 0: 256 x 256, BK  64   wave tile 128 x 64 = 8 x 4 blocks of v_mfma_i32_16x16x64_i8
-//   cfg 1: 128 x 128, BK 128   wave tile  64 x 32 = 4 x 2 blocks
-//   cfg 2:  64 x  64, BK 256   wave tile  32 x 16 = 2 x 1 blocks
-// Every stage moves 32 KB (2 x 16 B per thread per operand).  Operands go HBM -> VGPR -> LDS;
-// the VGPR staging is double-buffered so global loads are issued two k-stages ahead of their use,
-// LDS is double-buffered (one barrier per stage).  LDS rows hold BK bytes with the 16-byte chunk
-// index XOR-swizzled by the row, so the 16-lane groups of each ds_read_b128 fragment load hit
-// distinct banks.  Rows >= m / n and k >= kp are zero-filled (kp % 32 == 0: every 16-byte chunk
-// is wholly inside or outside), k steps wholly beyond kp are skipped.
+//   * inside an entry tiles are rastered in groups of 8 tile-rows, m fastest, so the compute
+//     units of an XCD share A and B panels in L2.
+// Workgroups of 256 threads = 4 waves in a 2 x 2 arrangement, two workgroups per compute unit
+// (one's epilogue and barrier waits overlap the other's MFMA work):
+//   cfg 0: 256 x 128 tile, wave tile 128 x 64 = 8 x 4 blocks of v_mfma_i32_16x16x64_i8
+//   cfg 1: 128 x 128 tile, wave tile  64 x 64 = 4 x 4 blocks
+//   cfg 2:  64 x  64 tile, wave tile  32 x 32 = 2 x 2 blocks
+// K advances in stages of 64.  Operands go HBM -> LDS directly (global_load_lds_dwordx4, no VGPR
+// round trip) into a ring of 3 LDS stages, two stages ahead of the MFMA work; one barrier per
+// stage.  An LDS row holds the 64 k-bytes of one A / B row as 4 chunks of 16 bytes, chunk index
+// XOR-swizzled by (row / 2) mod 4 so that the 16-lane groups of each 128-bit fragment read hit
+// distinct banks.  A DMA instruction fills 1 KB (16 rows): lane l writes chunk l mod 4 of row
+// l / 4 and so loads the global chunk that the swizzle puts there.
+// Fragment reads are issued as inline ds_read_b128 with a single lgkmcnt wait: the compiler would
+// otherwise place a vmcnt(0) before every LDS read that may alias an LDS DMA in flight, which
+// drains the prefetch ring.  The ring's own waits are explicit (s_waitcnt vmcnt(n) + s_barrier).
+// Bounds: rows >= m / n load (clamped) row m-1 / n-1 and only feed outputs that are not stored;
+// with kp % 64 == 32 the last stage's A chunks k >= kp are overwritten with zeros before use.
 // Epilogue, per problem: int32 C (the reference contract, used by the kernel-level API and the
-// abs plane), or -- in the production pipeline -- the CRT residue byte
-// y = ((C mod p) q) mod p of the plane's modulus p and CRT inverse q, which is all the
-// reconstruction needs from a residue plane; this cuts the plane write from 4 to 1 byte.
+// abs plane), or -- in the production pipeline -- one residue byte C mod p per entry (I8Epi),
+// which with q-folded A residues is the CRT digit; this cuts the plane write from 4 to 1 byte.
 #include <algorithm>
 #include <cstring>
 #include <mutex>
@@ -32,122 +37,90 @@
 
 #include "common.hpp"
 
+#define GGEMM_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+
 namespace ggemm {
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-constexpr int kThreads = 512;
+constexpr int kThreads = 256;
+constexpr int kBK = 64;
+constexpr int kStages = 3;
 constexpr int kChunk = 32;   // tiles per XCD chunk
 constexpr int kXcds = 8;
 constexpr int kGroupM = 8;   // tile-rows per raster group
 
-template <int BM_, int BN_, int BK_>
+template <int BM_, int BN_>
 struct Cfg {
-  static constexpr int BM = BM_, BN = BN_, BK = BK_;
-  static constexpr int WM = BM / 2, WN = BN / 4;     // wave tile (2 x 4 waves)
+  static constexpr int BM = BM_, BN = BN_;
+  static constexpr int WM = BM / 2, WN = BN / 2;     // wave tile (2 x 2 waves)
   static constexpr int FM = WM / 16, FN = WN / 16;   // 16 x 16 MFMA blocks per wave
-  static constexpr int CPR = BK / 16;                // 16-byte chunks per LDS row
-  static constexpr int LA = BM * CPR / kThreads;     // chunks per thread per stage
-  static constexpr int LB = BN * CPR / kThreads;
-  static constexpr int STAGE = (BM + BN) * BK;
-  static_assert(BM * CPR % kThreads == 0 && BN * CPR % kThreads == 0, "chunk split");
-  static_assert(FM >= 1 && FN >= 1, "wave tile");
+  static constexpr int SA = BM * kBK, SB = BN * kBK, STAGE = SA + SB;
+  static constexpr int PA = SA / 1024, PB = SB / 1024;   // 1 KB DMA pieces per operand and stage
+  static constexpr int DA = PA / 4, DB = PB / 4;         // per wave
+  static constexpr int VM = DA + DB;                     // DMA instructions per wave and stage
+  static_assert(PA % 4 == 0 && PB % 4 == 0 && FM >= 1 && FN >= 1, "tile split");
 };
-using Cfg0 = Cfg<256, 256, 64>;
-using Cfg1 = Cfg<128, 128, 128>;
-using Cfg2 = Cfg<64, 64, 256>;
-constexpr int kSmem = 2 * Cfg0::STAGE;   // 64 KB
-static_assert(2 * Cfg1::STAGE <= kSmem && 2 * Cfg2::STAGE <= kSmem, "smem");
+using Cfg0 = Cfg<256, 128>;
+using Cfg1 = Cfg<128, 128>;
+using Cfg2 = Cfg<64, 64>;
+constexpr int kSmem = kStages * Cfg0::STAGE;   // 72 KB: two workgroups per compute unit
+static_assert(Cfg1::STAGE <= Cfg0::STAGE && Cfg2::STAGE <= Cfg0::STAGE, "smem");
 
-template <int CPR>
-__device__ __forceinline__ int swz(int row, int ch) {
-  if constexpr (CPR == 4) return ch ^ ((row >> 1) & 3);
-  else return ch ^ (row & 7);
+__device__ __forceinline__ int swz(int row, int ch) { return ch ^ ((row >> 1) & 3); }
+
+// ds_read_b128 at LDS byte address addr + OFF
+template <int OFF>
+__device__ __forceinline__ v4i lds_read(uint32_t addr) {
+  v4i r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+  return r;
+}
+template <int F, int OFF0, int I = 0>
+__device__ __forceinline__ void read_frags(v4i* f, uint32_t addr) {
+  if constexpr (I < F) {
+    f[I] = lds_read<OFF0 + I * 1024>(addr);
+    read_frags<F, OFF0, I + 1>(f, addr);
+  }
+}
+// at most VM of this wave's LDS DMA instructions outstanding, LDS ops done, then the barrier
+template <int VM>
+__device__ __forceinline__ void wait_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(VM) : "memory");
 }
 
 template <class C>
-struct Stage {
-  uint4 a[C::LA], b[C::LB];
-};
+__device__ __forceinline__ void dma_stage(const int8_t* A, const int8_t* B, int kp, int m_rem, int n_rem, int k0,
+                                          uint8_t* st, int wave, int lane) {
+  const int r_in = lane >> 2, pc = lane & 3;
+#pragma unroll
+  for (int q = 0; q < C::DA; ++q) {
+    const int piece = wave + 4 * q, row = piece * 16 + r_in;
+    const int kk = k0 + 16 * swz(row, pc);
+    const int rr = row < m_rem ? row : m_rem - 1;
+    __builtin_amdgcn_global_load_lds((const void*)(A + (size_t)rr * kp + (kk < kp ? kk : 0)),
+                                     GGEMM_LDS(st + piece * 1024), 16, 0, 0);
+  }
+#pragma unroll
+  for (int q = 0; q < C::DB; ++q) {
+    const int piece = wave + 4 * q, row = piece * 16 + r_in;
+    const int kk = k0 + 16 * swz(row, pc);
+    const int rr = row < n_rem ? row : n_rem - 1;
+    __builtin_amdgcn_global_load_lds((const void*)(B + (size_t)rr * kp + (kk < kp ? kk : 0)),
+                                     GGEMM_LDS(st + C::SA + piece * 1024), 16, 0, 0);
+  }
+}
 
-template <class C>
-__device__ __forceinline__ void load_global(Stage<C>& s, const int8_t* A, const int8_t* B, int m_rem, int n_rem,
-                                            int kp, int k0, int tid) {
-#pragma unroll
-  for (int q = 0; q < C::LA; ++q) {
-    const int c = tid + q * kThreads, row = c / C::CPR, ch = c % C::CPR;
-    const int kk = k0 + ch * 16;
-    s.a[q] = (row < m_rem && kk < kp) ? *reinterpret_cast<const uint4*>(A + (size_t)row * kp + kk)
-                                      : make_uint4(0u, 0u, 0u, 0u);
-  }
-#pragma unroll
-  for (int q = 0; q < C::LB; ++q) {
-    const int c = tid + q * kThreads, row = c / C::CPR, ch = c % C::CPR;
-    const int kk = k0 + ch * 16;
-    s.b[q] = (row < n_rem && kk < kp) ? *reinterpret_cast<const uint4*>(B + (size_t)row * kp + kk)
-                                      : make_uint4(0u, 0u, 0u, 0u);
-  }
+__device__ __forceinline__ uint32_t residue_byte(int32_t c, const I8Epi& e) {
+  const uint32_t u = (uint32_t)c + e.bias;
+  int r = (int)(u - __umulhi(u, e.mc) * e.p);
+  return (uint32_t)(r + (r < 0 ? (int)e.p : 0));
 }
 
 template <class C>
-__device__ __forceinline__ void store_lds(int8_t* st, const Stage<C>& s, int tid) {
-  int8_t* sA = st;
-  int8_t* sB = st + C::BM * C::BK;
-#pragma unroll
-  for (int q = 0; q < C::LA; ++q) {
-    const int c = tid + q * kThreads, row = c / C::CPR, ch = c % C::CPR;
-    *reinterpret_cast<uint4*>(sA + row * C::BK + swz<C::CPR>(row, ch) * 16) = s.a[q];
-  }
-#pragma unroll
-  for (int q = 0; q < C::LB; ++q) {
-    const int c = tid + q * kThreads, row = c / C::CPR, ch = c % C::CPR;
-    *reinterpret_cast<uint4*>(sB + row * C::BK + swz<C::CPR>(row, ch) * 16) = s.b[q];
-  }
-}
-
-template <class C>
-__device__ __forceinline__ void mma_stage(const int8_t* st, int k0, int kp, int wm, int wn, int lane,
-                                          v4i (&acc)[C::FM][C::FN]) {
-  const int8_t* sA = st;
-  const int8_t* sB = st + C::BM * C::BK;
-  const int frow = lane & 15, fch = lane >> 4;
-#pragma unroll
-  for (int ks = 0; ks < C::BK / 64; ++ks) {
-    if (k0 + ks * 64 >= kp) break;   // block-uniform
-    const int ch = ks * 4 + fch;
-    v4i a[C::FM], b[C::FN];
-#pragma unroll
-    for (int i = 0; i < C::FM; ++i) {
-      const int row = wm * C::WM + i * 16 + frow;
-      a[i] = *reinterpret_cast<const v4i*>(sA + row * C::BK + swz<C::CPR>(row, ch) * 16);
-    }
-#pragma unroll
-    for (int j = 0; j < C::FN; ++j) {
-      const int row = wn * C::WN + j * 16 + frow;
-      b[j] = *reinterpret_cast<const v4i*>(sB + row * C::BK + swz<C::CPR>(row, ch) * 16);
-    }
-#pragma unroll
-    for (int i = 0; i < C::FM; ++i)
-#pragma unroll
-      for (int j = 0; j < C::FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], b[j], acc[i][j], 0, 0, 0);
-  }
-}
-
-__device__ __forceinline__ uint32_t mod_small(uint32_t u, uint32_t p, uint32_t magic) {
-  uint32_t r = u - __umulhi(u, magic) * p;   // magic = floor(2^32/p): quotient low by at most 1
-  r = r >= p ? r - p : r;
-  return r >= p ? r - p : r;
-}
-__device__ __forceinline__ uint32_t crt_digit(int32_t c, const I8Epi& e) {
-  const uint32_t uc = c < 0 ? 0u - (uint32_t)c : (uint32_t)c;
-  uint32_t r = mod_small(uc, e.p, e.magic);
-  if (c < 0 && r) r = e.p - r;
-  return mod_small(r * e.q, e.p, e.magic);
-}
-
-template <class C>
-__device__ __forceinline__ void run_tile(int8_t* smem, const i8_problem& P, const I8Epi& epi, int tm, int tn) {
+__device__ __forceinline__ void run_tile(uint8_t* lds, const i8_problem& P, const I8Epi& epi, int tm, int tn) {
+  constexpr int FM = C::FM, FN = C::FN;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
   const int row0 = tm * C::BM, col0 = tn * C::BN;
@@ -155,31 +128,55 @@ __device__ __forceinline__ void run_tile(int8_t* smem, const i8_problem& P, cons
   const int kp = P.kp;
   const int8_t* A = P.A + (size_t)row0 * kp;
   const int8_t* B = P.B + (size_t)col0 * kp;
-  const int nk = (kp + C::BK - 1) / C::BK;
+  const int nk = (kp + kBK - 1) / kBK;
 
-  v4i acc[C::FM][C::FN];
-#pragma unroll
-  for (int i = 0; i < C::FM; ++i)
-#pragma unroll
-    for (int j = 0; j < C::FN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+  // fragment addresses: rows wm WM + 16 i + lane % 16 (A), wn WN + 16 j + lane % 16 (B), chunk lane / 16;
+  // the swizzle depends on row / 2 mod 4 only, so blocks i, j sit at fixed 1 KB immediates
+  const int fr = lane & 15, fc = lane >> 4;
+  const uint32_t lbase = (uint32_t)(uintptr_t)GGEMM_LDS(lds);
+  const int ra = wm * C::WM + fr, rb = wn * C::WN + fr;
+  const uint32_t a_addr = lbase + ra * kBK + swz(ra, fc) * 16;
+  const uint32_t b_addr = lbase + rb * kBK + swz(rb, fc) * 16;
 
-  Stage<C> s0, s1;
-  load_global<C>(s0, A, B, m_rem, n_rem, kp, 0, tid);
-  if (nk > 1) load_global<C>(s1, A, B, m_rem, n_rem, kp, C::BK, tid);
-  store_lds<C>(smem, s0, tid);
-  __syncthreads();
-  // two k-stages per trip so that the staging set index is static: stage kt lives in LDS buffer
-  // kt & 1; its successor kt + 1 is in staging set (kt + 1) & 1; loads for kt + 2 reuse set kt & 1.
-  for (int kt = 0; kt < nk; kt += 2) {
-    if (kt + 2 < nk) load_global<C>(s0, A, B, m_rem, n_rem, kp, (kt + 2) * C::BK, tid);
-    mma_stage<C>(smem, kt * C::BK, kp, wm, wn, lane, acc);
-    if (kt + 1 < nk) store_lds<C>(smem + C::STAGE, s1, tid);
-    __syncthreads();
-    if (kt + 1 >= nk) break;
-    if (kt + 3 < nk) load_global<C>(s1, A, B, m_rem, n_rem, kp, (kt + 3) * C::BK, tid);
-    mma_stage<C>(smem + C::STAGE, (kt + 1) * C::BK, kp, wm, wn, lane, acc);
-    if (kt + 2 < nk) store_lds<C>(smem, s0, tid);
-    __syncthreads();
+  v4i acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+
+  dma_stage<C>(A, B, kp, m_rem, n_rem, 0, lds, wave, lane);
+  if (nk > 1) dma_stage<C>(A, B, kp, m_rem, n_rem, kBK, lds + C::STAGE, wave, lane);
+  int buf = 0;
+  for (int kt = 0; kt < nk; ++kt) {
+    // stage kt landed (stage kt + 1 may still be in flight) and every wave is done with kt - 1
+    if (kt + 1 < nk) wait_barrier<C::VM>(); else wait_barrier<0>();
+    if (kt + 2 < nk) {
+      const int b2 = buf == 0 ? 2 : buf - 1;   // (buf + 2) mod 3: the buffer of stage kt - 1
+      dma_stage<C>(A, B, kp, m_rem, n_rem, (kt + 2) * kBK, lds + b2 * C::STAGE, wave, lane);
+    }
+    uint8_t* st = lds + buf * C::STAGE;
+    if (kt == nk - 1 && (kp & 63)) {   // k in [kp, kp + 32): zero A's chunks 2, 3
+      for (int c = tid; c < C::BM * 2; c += kThreads) {
+        const int row = c >> 1, ch = 2 + (c & 1);
+        *reinterpret_cast<uint4*>(st + row * kBK + swz(row, ch) * 16) = make_uint4(0u, 0u, 0u, 0u);
+      }
+      wait_barrier<0>();
+    }
+    const uint32_t so = (uint32_t)(buf * C::STAGE);
+    v4i a[FM], b[FN];
+    read_frags<FN, C::SA>(b, b_addr + so);
+    read_frags<FM, 0>(a, a_addr + so);
+    // the fragments are valid after this wait: every fragment is an operand of it
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a[0]), "+v"(b[0]), "+v"(a[FM - 1]), "+v"(b[FN - 1]));
+#pragma unroll
+    for (int i = 1; i < FM - 1; ++i) asm volatile("" : "+v"(a[i]));
+#pragma unroll
+    for (int j = 1; j < FN - 1; ++j) asm volatile("" : "+v"(b[j]));
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], b[j], acc[i][j], 0, 0, 0);
+    buf = buf == 2 ? 0 : buf + 1;
   }
 
   // D block layout: lane l, register r -> row 4 (l / 16) + r, column l % 16; a lane's 4 values
@@ -187,9 +184,9 @@ __device__ __forceinline__ void run_tile(int8_t* smem, const i8_problem& P, cons
   const size_t ldc = (size_t)P.m;
   const bool vec = (P.m % 4 == 0) && ((reinterpret_cast<uintptr_t>(P.C) & (epi.mode ? 3 : 15)) == 0);
 #pragma unroll
-  for (int i = 0; i < C::FM; ++i)
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < C::FN; ++j) {
+    for (int j = 0; j < FN; ++j) {
       const int col = col0 + wn * C::WN + j * 16 + (lane & 15);
       const int r0 = row0 + wm * C::WM + i * 16 + 4 * (lane >> 4);
       if (col >= P.n || r0 >= P.m) continue;
@@ -207,7 +204,7 @@ __device__ __forceinline__ void run_tile(int8_t* smem, const i8_problem& P, cons
         uint8_t* out = reinterpret_cast<uint8_t*>(P.C) + (size_t)r0 + (size_t)col * ldc;
         uint32_t y[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) y[r] = crt_digit(v[r], epi);
+        for (int r = 0; r < 4; ++r) y[r] = residue_byte(v[r], epi);
         if (vec && r0 + 3 < P.m) {
           *reinterpret_cast<uint32_t*>(out) = y[0] | (y[1] << 8) | (y[2] << 16) | (y[3] << 24);
         } else {
@@ -219,10 +216,10 @@ __device__ __forceinline__ void run_tile(int8_t* smem, const i8_problem& P, cons
     }
 }
 
-__global__ void __launch_bounds__(kThreads) i8_grouped_kernel(const i8_problem* __restrict__ probs,
-                                                              const I8Epi* __restrict__ epis,
-                                                              const int* __restrict__ sched) {
-  extern __shared__ __align__(16) int8_t smem[];
+__global__ void __launch_bounds__(kThreads, 2) i8_grouped_kernel(const i8_problem* __restrict__ probs,
+                                                                 const I8Epi* __restrict__ epis,
+                                                                 const int* __restrict__ sched) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
   const int total = sched[0];
   const int ne = sched[1];
   // XCD-aware remap of the dispatch index (a permutation of [0, total))
@@ -247,8 +244,8 @@ __global__ void __launch_bounds__(kThreads) i8_grouped_kernel(const i8_problem* 
   const i8_problem P = probs[pi];
   I8Epi epi{0u, 1u, 0u, 0u};
   if (epis) epi = epis[pi];
-  const int edge = cfg == 0 ? 256 : (cfg == 1 ? 128 : 64);
-  const int tiles_m = (P.m + edge - 1) / edge, tiles_n = (P.n + edge - 1) / edge;
+  const int bm = i8_tile_m(cfg), bn = i8_tile_n(cfg);
+  const int tiles_m = (P.m + bm - 1) / bm, tiles_n = (P.n + bn - 1) / bn;
   // grouped raster: blocks of kGroupM tile-rows, m fastest inside a block
   const int per_group = kGroupM * tiles_n;
   const int g = local / per_group, first_m = g * kGroupM;
@@ -256,9 +253,9 @@ __global__ void __launch_bounds__(kThreads) i8_grouped_kernel(const i8_problem* 
   const int r = local - g * per_group;
   const int tm = first_m + r % gsz, tn = r / gsz;
   switch (cfg) {
-    case 0: run_tile<Cfg0>(smem, P, epi, tm, tn); break;
-    case 1: run_tile<Cfg1>(smem, P, epi, tm, tn); break;
-    default: run_tile<Cfg2>(smem, P, epi, tm, tn); break;
+    case 0: run_tile<Cfg0>(lds, P, epi, tm, tn); break;
+    case 1: run_tile<Cfg1>(lds, P, epi, tm, tn); break;
+    default: run_tile<Cfg2>(lds, P, epi, tm, tn); break;
   }
 }
 
@@ -278,8 +275,8 @@ bool valid_problem(const i8_problem& p) {
   return (reinterpret_cast<uintptr_t>(p.C) & 3) == 0;
 }
 int tiles_of(int cfg, int m, int n) {
-  const int e = i8_tile_edge(cfg);
-  return ((m + e - 1) / e) * ((n + e - 1) / e);
+  const int bm = i8_tile_m(cfg), bn = i8_tile_n(cfg);
+  return ((m + bm - 1) / bm) * ((n + bn - 1) / bn);
 }
 // Automatic tile: least padded work per unit efficiency (relative efficiencies 1, 0.7, 0.35).
 int auto_cfg(int m, int n) {
@@ -287,8 +284,7 @@ int auto_cfg(int m, int n) {
   int best = 0;
   double best_cost = 1e300;
   for (int c = 0; c < kI8NumCfg; ++c) {
-    const double b = i8_tile_edge(c);
-    const double cost = tiles_of(c, m, n) * b * b / eff[c];
+    const double cost = tiles_of(c, m, n) * (double)i8_tile_m(c) * i8_tile_n(c) / eff[c];
     if (cost < best_cost) { best_cost = cost; best = c; }
   }
   return best;
@@ -308,20 +304,19 @@ int i8_build_schedule(const i8_problem* h, int num, void* h_ws, size_t ws_bytes,
     int c = h[i].tile_cfg;
     if (c < 0) c = auto_cfg(h[i].m, h[i].n);
     if (c >= kI8NumCfg) c = kI8NumCfg - 1;
-    const double b = i8_tile_edge(c);
-    ents.push_back({b * b * (double)(h[i].kp + 128), tiles_of(c, h[i].m, h[i].n), i, c});
+    ents.push_back({(double)i8_tile_m(c) * i8_tile_n(c) * (double)(h[i].kp + 128), tiles_of(c, h[i].m, h[i].n), i, c});
   }
-  // group-level fill: fewer tiles than compute units -> shrink automatic tiles one step
+  // group-level fill: fewer tiles than workgroup slots (2 per compute unit) -> shrink automatic
+  // tiles one step
   for (int pass = 0; pass < 2; ++pass) {
     long long t = 0;
     for (auto& e : ents) t += e.tiles;
-    if (t >= num_cus) break;
+    if (t >= 2LL * num_cus) break;
     for (auto& e : ents)
       if (e.cfg < kI8NumCfg - 1 && h[e.prob].tile_cfg < 0) {
         ++e.cfg;
-        const double b = i8_tile_edge(e.cfg);
         e.tiles = tiles_of(e.cfg, h[e.prob].m, h[e.prob].n);
-        e.cost = b * b * (double)(h[e.prob].kp + 128);
+        e.cost = (double)i8_tile_m(e.cfg) * i8_tile_n(e.cfg) * (double)(h[e.prob].kp + 128);
       }
   }
   std::stable_sort(ents.begin(), ents.end(), [](const Ent& a, const Ent& b) {
@@ -356,6 +351,21 @@ int i8_launch(const i8_problem* d_probs, const I8Epi* d_epi, const void* d_sched
   if (!info) return 1;
   if (info->num_launches == 0 || info->tiles_main == 0) return 0;
   if (!d_probs || !d_sched) return 1;
+  // 72 KB of dynamic LDS exceeds the default limit: raise it once per device
+  static std::mutex attr_mu;
+  static std::vector<int> attr_done;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 6;
+  {
+    std::lock_guard<std::mutex> lk(attr_mu);
+    if ((int)attr_done.size() <= dev) attr_done.resize(dev + 1, 0);
+    if (!attr_done[dev]) {
+      if (hipFuncSetAttribute((const void*)i8_grouped_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kSmem) !=
+          hipSuccess)
+        return 6;
+      attr_done[dev] = 1;
+    }
+  }
   hipLaunchKernelGGL(i8_grouped_kernel, dim3((unsigned)info->tiles_main), dim3(kThreads), kSmem, s, d_probs, d_epi,
                      static_cast<const int*>(d_sched));
   return hipGetLastError() == hipSuccess ? 0 : 6;

@@ -391,13 +391,19 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
 
 __global__ void __launch_bounds__(kThreads) prep_kernel(const oz2_problem* __restrict__ probs, int a_blocks,
                                                         const CrtTables* __restrict__ tab,
-                                                        unsigned long long* __restrict__ cnt) {
+                                                        unsigned long long* __restrict__ cnt, int fold_q) {
   __shared__ PrepShared sm;
   const oz2_problem& pr = probs[blockIdx.y];
   const int N = pr.num_moduli;
   if (N < 1 || N > kMaxModuli || pr.alpha == 0.0) return;   // alpha == 0: A, B never referenced
-  for (int q = threadIdx.x; q < kMaxModuli * kPow2Table; q += kThreads)
-    (&sm.pow2[0][0])[q] = tab->pow2[q / kPow2Table][q % kPow2Table];
+  const bool fold = fold_q && (int)blockIdx.x < a_blocks;
+  // 2^e mod p; for folded A residues (q 2^e) mod p, so that sum c_i [q 2^(E_i)] = q x (mod p)
+  for (int q = threadIdx.x; q < kMaxModuli * kPow2Table; q += kThreads) {
+    const int l = q / kPow2Table;
+    uint32_t v = tab->pow2[l][q % kPow2Table];
+    if (fold && l < N) v = (v * (uint32_t)tab->qinv[N][l]) % (uint32_t)tab->p[l];
+    (&sm.pow2[0][0])[q] = (uint8_t)v;
+  }
   if (threadIdx.x < kMaxModuli) {
     sm.p[threadIdx.x] = (uint32_t)tab->p[threadIdx.x];
     sm.magic[threadIdx.x] = tab->magic[threadIdx.x];
@@ -416,7 +422,7 @@ int g_force_split = 0;
 
 }  // namespace
 
-int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t s) {
+int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t s, int fold_q) {
   if (num <= 0) return 0;
   if (num > 65535 || max_m < 0 || max_n < 0) return 1;
   DevCtx* c = dev_ctx();
@@ -429,14 +435,14 @@ int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t
   int S = (int)std::min<long long>(16, std::max<long long>(1, (target + blocks - 1) / blocks));
   if (g_force_split > 0) S = g_force_split;
   hipLaunchKernelGGL(prep_kernel, dim3(a_blocks + b_blocks, num, S), dim3(kThreads), 0, s, d, a_blocks,
-                     c->tab, c->counters);
+                     c->tab, c->counters, fold_q);
   return hipGetLastError() == hipSuccess ? 0 : 3;
 }
 
 }  // namespace ggemm
 
 extern "C" int oz2_prep_grouped(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t s) {
-  return ggemm::prep_launch(d, num, max_m, max_n, s);
+  return ggemm::prep_launch(d, num, max_m, max_n, s, 0);
 }
 
 extern "C" void oz2_debug_force_prep_split(int S) { ggemm::g_force_split = (S >= 1 && S <= 64) ? S : 0; }
