@@ -26,6 +26,10 @@ inline int kp_of(int k) { return (int)align_up((size_t)k, kKpAlign); }
 struct CrtTables {
   int32_t p[kMaxModuli];
   uint32_t magic[kMaxModuli];                  // floor(2^32 / p)
+  double inv_p_up[kMaxModuli];                 // 1 / p rounded up to a double
+  int32_t Kp[kMaxModuli];                      // p ceil(2^28 / p)
+  double h_ip_up[kMaxModuli];                  // floor(p / 2) inv_p_up, rounded up
+  int32_t w3[kMaxModuli + 1][kMaxModuli][3];   // [0][l]: 2^(18 i) mod p_l; [N][l]: q_(N,l) 2^(18 i) mod p_l
   uint8_t pow2[kMaxModuli][kPow2Table];        // 2^e mod p
   uint64_t s1[kMaxModuli + 1][kMaxModuli];     // floor(M_l / u1)
   uint32_t s2[kMaxModuli + 1][kMaxModuli];     // round(frac(M_l / u1) 2^18)

@@ -88,8 +88,16 @@ int build(CrtTables* t) {
     const uint32_t p = (uint32_t)kModuli[l];
     t->p[l] = (int32_t)p;
     t->magic[l] = (uint32_t)((1ull << 32) / p);
+    double ip = 1.0 / (double)p;
+    if (std::fma(ip, (double)p, -1.0) < 0.0) ip = std::nextafter(ip, 1.0);   // fma is exact here
+    t->inv_p_up[l] = ip;
+    t->Kp[l] = (int32_t)(p * (((1u << 28) + p - 1) / p));
+    double hip = (double)(p / 2) * ip;
+    if (std::fma((double)(p / 2), ip, -hip) > 0.0) hip = std::nextafter(hip, 1.0);
+    t->h_ip_up[l] = hip;
     uint32_t v = 1 % p;
     for (int e = 0; e < kPow2Table; ++e) { t->pow2[l][e] = (uint8_t)v; v = (2 * v) % p; }
+    for (int i = 0; i < 3; ++i) t->w3[0][l][i] = t->pow2[l][18 * i];
   }
   for (int N = 1; N <= kMaxModuli; ++N) {
     U192 P;
@@ -106,6 +114,8 @@ int build(CrtTables* t) {
         if ((mr * x) % p == 1 % p) { inv = (int)x; break; }
       if (inv < 0) return 4;
       t->qinv[N][l] = inv;
+      for (int i = 0; i < 3; ++i)
+        t->w3[N][l][i] = (int32_t)(((uint32_t)t->pow2[l][18 * i] * (uint32_t)inv) % (uint32_t)kModuli[l]);
       top = std::max(top, bit_length(M[l]));
     }
     const int sh = top - 49;   // u1 = 2^sh keeps every M_l / u1 below 2^49

@@ -112,13 +112,58 @@ __device__ __forceinline__ Split split_int(double x) {
   d.E = E;
   return d;
 }
-__device__ __forceinline__ uint32_t residue_u8(const Split& d, uint32_t p, uint32_t magic, const uint8_t* pw) {
-  const uint32_t s = d.c0 * pw[d.E] + d.c1 * pw[d.E + 18] + d.c2 * pw[d.E + 36];   // < 2^28
-  uint32_t r = s - __umulhi(s, magic) * p;                                         // < 2p
-  r = r >= p ? r - p : r;
-  if (d.neg && r) r = p - r;
-  const int ri = (int)r > (int)((p - 1) >> 1) ? (int)r - (int)p : (int)r;
-  return (uint32_t)(uint8_t)(int8_t)ri;
+// Symmetric residues sym(x mod p) in [-h, p - 1 - h] (h = floor(p / 2)) of integers
+// x = c0 2^E + c1 2^(E+18) + c2 2^(E+36) given as signed 18-bit chunks (the sign of x on each):
+//   u = c0 w0 + c1 w1 + c2 w2 + K p,  w_i = 2^(E + 18 i) mod p (times q for folded planes)
+//       (24-bit multiply-adds; |c_i w_i| < 2^26, K p >= 2^28, so 0 < u < 2^30)
+//   q = trunc(fma(u, ip, hip)) = floor((u + h) / p)
+//       exact: ip = 1/p and hip = h ip are rounded up, so the fma's exact value is >= (u + h)/p,
+//       and it exceeds it by less than 2^-21 / p while (u + h)/p <= floor + 1 - 1/p
+//   r = fma(-q, p, u)                 (exact: an integer in [-h, p - 1 - h])
+// The byte equals the reference's reduce / negate / symmetric-map sequence; every operation is
+// full rate (24-bit integer and FP64 arithmetic, no 32-bit integer multiply).  When no lane of the
+// wave has E > 0 the weights are per-plane constants (scalar registers), otherwise per-element
+// LDS table lookups.
+struct PlaneC {
+  int Kp, w0, w1, w2;
+  double p, ip, hip;
+};
+__device__ __forceinline__ PlaneC plane_c(const CrtTables* __restrict__ tab, int l, int widx) {
+  return PlaneC{tab->Kp[l], tab->w3[widx][l][0], tab->w3[widx][l][1], tab->w3[widx][l][2],
+                (double)tab->p[l], tab->inv_p_up[l], tab->h_ip_up[l]};
+}
+template <int NE>
+__device__ __forceinline__ void residue_bytes(const int* c0, const int* c1, const int* c2, const int* E, bool anyE,
+                                              const PlaneC& k, const uint8_t* pw, uint32_t* out) {
+  int u[NE];
+  if (!anyE) {
+#pragma unroll
+    for (int e = 0; e < NE; ++e) u[e] = __mul24(c0[e], k.w0) + __mul24(c1[e], k.w1) + __mul24(c2[e], k.w2) + k.Kp;
+  } else {
+#pragma unroll
+    for (int e = 0; e < NE; ++e)
+      u[e] = __mul24(c0[e], (int)pw[E[e]]) + __mul24(c1[e], (int)pw[E[e] + 18]) + __mul24(c2[e], (int)pw[E[e] + 36]) + k.Kp;
+  }
+#pragma unroll
+  for (int w = 0; w < NE / 4; ++w) {
+    uint32_t v = 0u;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const double ud = (double)u[4 * w + e];
+      const double q = trunc(fma(ud, k.ip, k.hip));
+      const int r = (int)fma(-q, k.p, ud);
+      v |= ((uint32_t)r & 0xffu) << (8 * e);
+    }
+    out[w] = v;
+  }
+}
+// signed chunks of an integer-valued double (|x| < 2^81)
+__device__ __forceinline__ void chunks(double x, int& c0, int& c1, int& c2, int& E) {
+  const Split d = split_int(x);
+  c0 = d.neg ? -(int)d.c0 : (int)d.c0;
+  c1 = d.neg ? -(int)d.c1 : (int)d.c1;
+  c2 = d.neg ? -(int)d.c2 : (int)d.c2;
+  E = d.E;
 }
 __device__ __forceinline__ uint32_t abs_u8(double a, int sig) {
   if (sig == OZ2_SHIFT_ZERO) return 0;
@@ -127,7 +172,6 @@ __device__ __forceinline__ uint32_t abs_u8(double a, int sig) {
 
 struct PrepShared {
   uint8_t pow2[kMaxModuli][kPow2Table];
-  uint32_t p[kMaxModuli], magic[kMaxModuli];
   double red0[kChains][kARows];
   double red1[kChains][kARows];
   int shift[kARows], sig[kARows];
@@ -137,7 +181,7 @@ struct PrepShared {
 
 // ------------------------------------------------------------------------------- A rows
 __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ tab, int blk, int split,
-                          int nsplit, PrepShared& sm, unsigned long long* cnt) {
+                          int nsplit, PrepShared& sm, unsigned long long* cnt, int widx) {
   const int tid = threadIdx.x;
   const int N = pr.num_moduli, K = pr.k, Kp = pr.kp, m = pr.m;
   const int row0 = blk * kARows;
@@ -245,19 +289,18 @@ __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ t
         for (int l = 0; l <= N; ++l)
           *reinterpret_cast<uint4*>(dst + (size_t)l * pr.a8_mod_stride) = make_uint4(0u, 0u, 0u, 0u);
       } else {
-        Split d[16];
+        int c0[16], c1[16], c2[16], E[16];
+        int anyE = 0;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) d[e] = split_int(trunc(mul_pow2(sm.tile[16 * seg + e][rr], sh_r)));
+        for (int e = 0; e < 16; ++e) {
+          chunks(trunc(mul_pow2(sm.tile[16 * seg + e][rr], sh_r)), c0[e], c1[e], c2[e], E[e]);
+          anyE |= E[e];
+        }
+        const bool wE = __any(anyE != 0);
         for (int l = 0; l < N; ++l) {
-          const uint32_t p = sm.p[l], mg = sm.magic[l];
-          const uint8_t* pw = sm.pow2[l];
+          const PlaneC pc = plane_c(tab, l, widx);
           uint32_t q[4];
-#pragma unroll
-          for (int w = 0; w < 4; ++w) {
-            q[w] = 0u;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) q[w] |= residue_u8(d[4 * w + e], p, mg, pw) << (8 * e);
-          }
+          residue_bytes<16>(c0, c1, c2, E, wE, pc, sm.pow2[l], q);
           *reinterpret_cast<uint4*>(dst + (size_t)l * pr.a8_mod_stride) = make_uint4(q[0], q[1], q[2], q[3]);
         }
         uint32_t q[4];
@@ -338,7 +381,8 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
   const int nchunk = (Kp + 127) / 128;
   const int per = (nchunk + nsplit - 1) / nsplit;
   const int c0 = min(nchunk, split * per), c1 = min(nchunk, c0 + per);
-  // split 0 walks every chunk (ordered sums) but writes residues only for its own range
+  // split 0 walks every chunk (ordered sums) but writes residues only for its own range; lane L
+  // owns k = 128 ch + 4 L + e
   for (int ch = (split == 0 ? 0 : c0); ch < (split == 0 ? nchunk : c1); ++ch) {
     const int k0 = 128 * ch + 4 * lane;
     if (k0 >= Kp) continue;
@@ -351,7 +395,8 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
         for (int l = 0; l <= N; ++l) *reinterpret_cast<uint32_t*>(base + (size_t)l * pr.b8_mod_stride + k0) = 0u;
       continue;
     }
-    Split d[4];
+    int q0[4], q1[4], q2[4], E[4];
+    int anyE = 0;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const double xs = mul_pow2(a[e], sh);
@@ -361,15 +406,14 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
         da2 = fma(fr, fr, da2);
         na2 = fma(xt, xt, na2);
       }
-      d[e] = split_int(xt);
+      chunks(xt, q0[e], q1[e], q2[e], E[e]);
+      anyE |= E[e];
     }
     if (!write) continue;
+    const bool wE = __any(anyE != 0);
     for (int l = 0; l < N; ++l) {
-      const uint32_t p = sm.p[l], mg = sm.magic[l];
-      const uint8_t* pw = sm.pow2[l];
-      uint32_t q = 0u;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) q |= residue_u8(d[e], p, mg, pw) << (8 * e);
+      uint32_t q;
+      residue_bytes<4>(q0, q1, q2, E, wE, plane_c(tab, l, 0), sm.pow2[l], &q);
       *reinterpret_cast<uint32_t*>(base + (size_t)l * pr.b8_mod_stride + k0) = q;
     }
     uint32_t q = 0u;
@@ -404,15 +448,11 @@ __global__ void __launch_bounds__(kThreads) prep_kernel(const oz2_problem* __res
     if (fold && l < N) v = (v * (uint32_t)tab->qinv[N][l]) % (uint32_t)tab->p[l];
     (&sm.pow2[0][0])[q] = (uint8_t)v;
   }
-  if (threadIdx.x < kMaxModuli) {
-    sm.p[threadIdx.x] = (uint32_t)tab->p[threadIdx.x];
-    sm.magic[threadIdx.x] = tab->magic[threadIdx.x];
-  }
   __syncthreads();
   const int blk = (int)blockIdx.x;
   if (blk < a_blocks) {
     if (blk * kARows >= pr.m) return;
-    prep_rows(pr, tab, blk, blockIdx.z, gridDim.z, sm, cnt);
+    prep_rows(pr, tab, blk, blockIdx.z, gridDim.z, sm, cnt, fold ? N : 0);
   } else {
     prep_cols(pr, tab, blk - a_blocks, blockIdx.z, gridDim.z, sm, cnt);
   }
