@@ -72,6 +72,19 @@ def fill(torch, out, phi, seed, salt, lo_hi=None):
         out.view(-1)[s0:s0 + cnt] = v
 
 
+def measured_traffic(workload):
+    """HBM bytes per INT8 GEMM launch from the committed rocprofv3 counter summary
+    (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by its plain-copy calibration), or None."""
+    f = REPO / "profiles" / "hbm_traffic.json"
+    try:
+        rec = json.loads(f.read_text()).get(workload)
+    except (OSError, ValueError):
+        return None
+    if not rec or rec.get("kernel") != "i8_grouped_kernel":
+        return None
+    return rec.get("traffic_bytes")
+
+
 def kp_of(k):
     return (k + 31) // 32 * 32
 
@@ -84,6 +97,8 @@ def main():
     ap.add_argument("--workload", default="uniform", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-native", action="store_true")
+    ap.add_argument("--probe-copy", action="store_true",
+                    help="only run a plain 1 GiB device copy 5 times (calibrates the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -91,6 +106,14 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.probe_copy:
+        src = torch.ones(1 << 30, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"probe": "copy", "bytes_read": 1 << 30, "bytes_written": 1 << 30, "launches": 5}))
+        return
     import ggemm as G
 
     W = WORKLOADS[args.workload]
@@ -160,7 +183,8 @@ def main():
     i8_ms = st_ms[1]
     achieved = int8_ops / (i8_ms * 1e-3) / 1e12 if i8_ms > 0 else 0.0
     prep_bytes = Gp * (8.0 * (m * k + n * k) + planes * (m + n) * kp_of(k) + 16.0 * (m + n))
-    recon_bytes = Gp * (4.0 * planes * m * n + 8.0 * m * n * (2 if W["beta"] != 0 else 1) + 16.0 * (m + n))
+    # reconstruct: N digit bytes + the int32 abs-plane product per entry, C0 (beta != 0), C, shifts
+    recon_bytes = Gp * ((N + 4.0) * m * n + 8.0 * m * n * (2 if W["beta"] != 0 else 1) + 16.0 * (m + n))
 
     h.close()   # free the timing workspace before the validation handle allocates its own
 
@@ -258,7 +282,7 @@ def main():
                           "reconstruct": round(recon_bytes / (st_ms[2] * 1e-3) / 1e9, 1) if st_ms[2] else None},
         "roofline": {"bound": "mfma", "kernel": "i8_grouped_kernel", "achieved": round(achieved, 2),
                      "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s", "frac": round(achieved / INT8_PEAK_TOPS, 4),
-                     "traffic": None},
+                     "traffic": measured_traffic(args.workload)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))
