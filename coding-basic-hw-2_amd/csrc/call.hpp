@@ -21,6 +21,7 @@ struct GroupedCall {
   int max_m = 0, max_n = 0;
   BlobLayout L{};
   i8_sched_info i8info{};
+  int i8_kernel = kI8General;     // INT8 GEMM kernel the schedule was built for
   int f64_tiles = 0;
   size_t h2d_bytes = 0;           // bytes of the blob to copy
 };

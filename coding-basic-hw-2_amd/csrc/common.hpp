@@ -66,7 +66,8 @@ struct F64Problem {
 };
 
 // Schedule image shared by the tile-based kernels (INT8 GEMM, FP64 GEMM):
-//   int[0] total tiles, int[1] entries, int[2..7] reserved,
+//   int[0] total tiles, int[1] entries, int[2] tiles per entry when all entries have the same
+//   count (INT8 GEMM; 0 otherwise), int[3..7] reserved,
 //   prefix[entries + 1] (first tile of each entry), entry[entries] = (problem << 2) | cfg.
 constexpr int kSchedHdr = 8;
 inline size_t sched_bytes(int entries) {
@@ -78,24 +79,25 @@ constexpr int kI8NumCfg = 3;
 __host__ __device__ inline int i8_tile_m(int cfg) { return cfg == 0 ? 256 : (cfg == 1 ? 128 : 64); }
 __host__ __device__ inline int i8_tile_n(int cfg) { return cfg == 0 ? 128 : (cfg == 1 ? 128 : 64); }
 // Per-product epilogue of the INT8 GEMM: mode 0 stores the int32 product (C is int32*, ld m);
-// mode 1 stores one byte per entry, the residue C mod p in [0, p), computed as
-// u = C + bias (bias = p ceil(2^31 / p), so 0 <= u < 2^32), u - p umulhi(u, mc) (mc = ceil(2^32 / p)),
-// plus p when that is negative.  In the production pipeline the A residues of plane l carry the
-// CRT inverse q_l (prep with fold_q), so this byte is the CRT digit y_l = (C_l q_l) mod p_l.
+// mode 1 stores one byte per entry, the residue C mod p in [0, p), from u = C + bias in [0, 2^32)
+// (bias = p ceil(2^31 / p)) by a Barrett step with mc = ceil(2^32 / p) and one correction.
+// In the production pipeline the A residues of plane l carry the CRT inverse q_l (prep with
+// fold_q), so this byte is the CRT digit y_l = (C_l q_l) mod p_l.
 struct I8Epi {
   uint32_t mode, p, mc, bias;
 };
-inline I8Epi i8_epi_residue(uint32_t p) {
-  const uint32_t mc = (uint32_t)((4294967296ull + p - 1) / p);
-  const uint32_t bias = p * (uint32_t)((2147483648ull + p - 1) / p);
-  return I8Epi{1u, p, mc, bias};
-}
+I8Epi i8_epi_residue(uint32_t p);
+// INT8 GEMM kernels: the general one (tile configs 0..2, two workgroups per compute unit) and the
+// large-tile one (every tile 256 x 256, one 8-wave workgroup per compute unit).
+enum { kI8General = 0, kI8Large = 1 };
 // Builds the INT8 schedule (LPT order); cfg < 0 in a problem selects automatically.
+// allow_large: the large-tile kernel may be chosen (when every product is on automatic large
+// tiles and they fill the GPU); *kernel receives the choice, which i8_launch must be given.
 int i8_build_schedule(const i8_problem* h, int num, void* h_ws, size_t ws_bytes, i8_sched_info* info,
-                      int num_cus);
+                      int num_cus, int allow_large = 0, int* kernel = nullptr);
 // d_epi: per-problem epilogues in device memory, or nullptr for int32 products everywhere.
 int i8_launch(const i8_problem* d_probs, const I8Epi* d_epi, const void* d_sched, const i8_sched_info* info,
-              hipStream_t s);
+              hipStream_t s, int kernel = kI8General);
 
 // Where the reconstruct reads a problem's plane products in the production pipeline: CRT digits
 // y_l (one byte per entry, plane l at Y + l * y_stride, ld m) and the abs-plane product L (int32).

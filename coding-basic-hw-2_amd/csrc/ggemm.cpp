@@ -228,7 +228,7 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
   }
   for (int i = 0; i < c.nn; ++i) hf[i] = f64_of(probs[nat_idx[i]]);
   if (c.nn && f64_build_schedule(hf, c.nn, hb + c.L.off_sf64, s_f64, &c.f64_tiles, nullptr)) return GGEMM_ERR_INVALID;
-  if (c.ne && i8_build_schedule(hi8, (int)c.n_i8, hb + c.L.off_si8, s_i8, &c.i8info, h->num_cus))
+  if (c.ne && i8_build_schedule(hi8, (int)c.n_i8, hb + c.L.off_si8, s_i8, &c.i8info, h->num_cus, 1, &c.i8_kernel))
     return GGEMM_ERR_I8GEMM;
   c.h2d_bytes = c.ne ? c.L.off_si8 + c.i8info.bytes_used : c.L.off_si8;
   *out = c;
@@ -244,7 +244,7 @@ int enqueue_grouped(const GroupedCall& c, const char* db, hipStream_t s, int rep
     ++*launches;
     prof::mark(prof_set, 1, s);
     if (i8_launch(reinterpret_cast<const i8_problem*>(db + c.L.off_i8), reinterpret_cast<const I8Epi*>(db + c.L.off_epi),
-                  db + c.L.off_si8, &c.i8info, s))
+                  db + c.L.off_si8, &c.i8info, s, c.i8_kernel))
       return GGEMM_ERR_I8GEMM;
     *launches += c.i8info.num_launches;
     prof::mark(prof_set, 2, s);

@@ -31,6 +31,7 @@
 // abs plane), or -- in the production pipeline -- one residue byte C mod p per entry (I8Epi),
 // which with q-folded A residues is the CRT digit; this cuts the plane write from 4 to 1 byte.
 #include <algorithm>
+#include <cmath>
 #include <cstring>
 #include <mutex>
 #include <vector>
@@ -44,29 +45,36 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-constexpr int kThreads = 256;
 constexpr int kBK = 64;
-constexpr int kStages = 3;
 constexpr int kChunk = 32;   // tiles per XCD chunk
 constexpr int kXcds = 8;
 constexpr int kGroupM = 8;   // tile-rows per raster group
 
-template <int BM_, int BN_>
+// Tile BM x BN computed by WGM x WGN waves through an NST-stage LDS ring.
+template <int BM_, int BN_, int WGM_, int WGN_, int NST_>
 struct Cfg {
-  static constexpr int BM = BM_, BN = BN_;
-  static constexpr int WM = BM / 2, WN = BN / 2;     // wave tile (2 x 2 waves)
-  static constexpr int FM = WM / 16, FN = WN / 16;   // 16 x 16 MFMA blocks per wave
+  static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_, NST = NST_;
+  static constexpr int NW = WGM * WGN, NT = 64 * NW;
+  static constexpr int WM = BM / WGM, WN = BN / WGN;   // wave tile
+  static constexpr int FM = WM / 16, FN = WN / 16;     // 16 x 16 MFMA blocks per wave
   static constexpr int SA = BM * kBK, SB = BN * kBK, STAGE = SA + SB;
-  static constexpr int PA = SA / 1024, PB = SB / 1024;   // 1 KB DMA pieces per operand and stage
-  static constexpr int DA = PA / 4, DB = PB / 4;         // per wave
-  static constexpr int VM = DA + DB;                     // DMA instructions per wave and stage
-  static_assert(PA % 4 == 0 && PB % 4 == 0 && FM >= 1 && FN >= 1, "tile split");
+  static constexpr int PA = SA / 1024, PB = SB / 1024; // 1 KB DMA pieces per operand and stage
+  static constexpr int DA = PA / NW, DB = PB / NW;     // per wave
+  static constexpr int VM = DA + DB;                   // DMA instructions per wave and stage
+  static constexpr int SMEM = NST * STAGE;
+  static_assert(PA % NW == 0 && PB % NW == 0 && FM >= 1 && FN >= 1, "tile split");
 };
-using Cfg0 = Cfg<256, 128>;
-using Cfg1 = Cfg<128, 128>;
-using Cfg2 = Cfg<64, 64>;
-constexpr int kSmem = kStages * Cfg0::STAGE;   // 72 KB: two workgroups per compute unit
-static_assert(Cfg1::STAGE <= Cfg0::STAGE && Cfg2::STAGE <= Cfg0::STAGE, "smem");
+// general kernel: 256 threads, two workgroups per compute unit (72 KB of LDS each)
+using Cfg0 = Cfg<256, 128, 2, 2, 3>;
+using Cfg1 = Cfg<128, 128, 2, 2, 3>;
+using Cfg2 = Cfg<64, 64, 2, 2, 3>;
+constexpr int kThreads = 256;
+constexpr int kSmem = Cfg0::SMEM;
+static_assert(Cfg1::SMEM <= kSmem && Cfg2::SMEM <= kSmem, "smem");
+// large-tile kernel: 512 threads, one workgroup per compute unit, 128 KB ring
+using CfgL = Cfg<256, 256, 2, 4, 4>;
+constexpr int kThreadsL = CfgL::NT;
+constexpr int kSmemL = CfgL::SMEM;
 
 __device__ __forceinline__ int swz(int row, int ch) { return ch ^ ((row >> 1) & 3); }
 
@@ -96,7 +104,7 @@ __device__ __forceinline__ void dma_stage(const int8_t* A, const int8_t* B, int 
   const int r_in = lane >> 2, pc = lane & 3;
 #pragma unroll
   for (int q = 0; q < C::DA; ++q) {
-    const int piece = wave + 4 * q, row = piece * 16 + r_in;
+    const int piece = wave + C::NW * q, row = piece * 16 + r_in;
     const int kk = k0 + 16 * swz(row, pc);
     const int rr = row < m_rem ? row : m_rem - 1;
     __builtin_amdgcn_global_load_lds((const void*)(A + (size_t)rr * kp + (kk < kp ? kk : 0)),
@@ -104,7 +112,7 @@ __device__ __forceinline__ void dma_stage(const int8_t* A, const int8_t* B, int 
   }
 #pragma unroll
   for (int q = 0; q < C::DB; ++q) {
-    const int piece = wave + 4 * q, row = piece * 16 + r_in;
+    const int piece = wave + C::NW * q, row = piece * 16 + r_in;
     const int kk = k0 + 16 * swz(row, pc);
     const int rr = row < n_rem ? row : n_rem - 1;
     __builtin_amdgcn_global_load_lds((const void*)(B + (size_t)rr * kp + (kk < kp ? kk : 0)),
@@ -112,17 +120,20 @@ __device__ __forceinline__ void dma_stage(const int8_t* A, const int8_t* B, int 
   }
 }
 
+// C mod p in [0, p): u = C + bias in [0, 2^32) (bias = p ceil(2^31 / p)), q = umulhi(u, mc) with
+// mc = ceil(2^32 / p) is floor(u / p) or one more (u (mc - 2^32/p) < 2^32), r = u - q p, plus p
+// when that is negative.
 __device__ __forceinline__ uint32_t residue_byte(int32_t c, const I8Epi& e) {
   const uint32_t u = (uint32_t)c + e.bias;
-  int r = (int)(u - __umulhi(u, e.mc) * e.p);
+  const int r = (int)(u - __umulhi(u, e.mc) * e.p);
   return (uint32_t)(r + (r < 0 ? (int)e.p : 0));
 }
 
 template <class C>
 __device__ __forceinline__ void run_tile(uint8_t* lds, const i8_problem& P, const I8Epi& epi, int tm, int tn) {
-  constexpr int FM = C::FM, FN = C::FN;
+  constexpr int FM = C::FM, FN = C::FN, NST = C::NST;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave & 1, wn = wave >> 1;
+  const int wm = wave % C::WGM, wn = wave / C::WGM;
   const int row0 = tm * C::BM, col0 = tn * C::BN;
   const int m_rem = P.m - row0, n_rem = P.n - col0;
   const int kp = P.kp;
@@ -144,19 +155,22 @@ __device__ __forceinline__ void run_tile(uint8_t* lds, const i8_problem& P, cons
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
 
-  dma_stage<C>(A, B, kp, m_rem, n_rem, 0, lds, wave, lane);
-  if (nk > 1) dma_stage<C>(A, B, kp, m_rem, n_rem, kBK, lds + C::STAGE, wave, lane);
+#pragma unroll
+  for (int q = 0; q < NST - 1; ++q)
+    if (q < nk) dma_stage<C>(A, B, kp, m_rem, n_rem, q * kBK, lds + q * C::STAGE, wave, lane);
   int buf = 0;
   for (int kt = 0; kt < nk; ++kt) {
-    // stage kt landed (stage kt + 1 may still be in flight) and every wave is done with kt - 1
-    if (kt + 1 < nk) wait_barrier<C::VM>(); else wait_barrier<0>();
-    if (kt + 2 < nk) {
-      const int b2 = buf == 0 ? 2 : buf - 1;   // (buf + 2) mod 3: the buffer of stage kt - 1
-      dma_stage<C>(A, B, kp, m_rem, n_rem, (kt + 2) * kBK, lds + b2 * C::STAGE, wave, lane);
+    // stage kt landed (the NST - 2 stages after it may still be in flight; near the end fewer
+    // were issued, so wait for everything) and every wave is done with stage kt - 1
+    if (kt + NST - 2 < nk) wait_barrier<(NST - 2) * C::VM>(); else wait_barrier<0>();
+    if (kt + NST - 1 < nk) {
+      int b2 = buf + NST - 1;   // the ring slot of stage kt - 1
+      if (b2 >= NST) b2 -= NST;
+      dma_stage<C>(A, B, kp, m_rem, n_rem, (kt + NST - 1) * kBK, lds + b2 * C::STAGE, wave, lane);
     }
     uint8_t* st = lds + buf * C::STAGE;
     if (kt == nk - 1 && (kp & 63)) {   // k in [kp, kp + 32): zero A's chunks 2, 3
-      for (int c = tid; c < C::BM * 2; c += kThreads) {
+      for (int c = tid; c < C::BM * 2; c += C::NT) {
         const int row = c >> 1, ch = 2 + (c & 1);
         *reinterpret_cast<uint4*>(st + row * kBK + swz(row, ch) * 16) = make_uint4(0u, 0u, 0u, 0u);
       }
@@ -176,7 +190,7 @@ __device__ __forceinline__ void run_tile(uint8_t* lds, const i8_problem& P, cons
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], b[j], acc[i][j], 0, 0, 0);
-    buf = buf == 2 ? 0 : buf + 1;
+    buf = buf + 1 == NST ? 0 : buf + 1;
   }
 
   // D block layout: lane l, register r -> row 4 (l / 16) + r, column l % 16; a lane's 4 values
@@ -216,13 +230,14 @@ __device__ __forceinline__ void run_tile(uint8_t* lds, const i8_problem& P, cons
     }
 }
 
-__global__ void __launch_bounds__(kThreads, 2) i8_grouped_kernel(const i8_problem* __restrict__ probs,
-                                                                 const I8Epi* __restrict__ epis,
-                                                                 const int* __restrict__ sched) {
-  extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+// Tile of workgroup blockIdx.x: XCD-aware remap of the dispatch index (a permutation of
+// [0, total)) and entry lookup in the prefix table; `local` is the tile index inside the entry.
+struct TileRef {
+  int pi, cfg, local;
+};
+__device__ __forceinline__ TileRef find_tile(const int* __restrict__ sched) {
   const int total = sched[0];
   const int ne = sched[1];
-  // XCD-aware remap of the dispatch index (a permutation of [0, total))
   const int b = blockIdx.x;
   const int span = kXcds * kChunk;
   const int full = total / span * span;
@@ -233,30 +248,61 @@ __global__ void __launch_bounds__(kThreads, 2) i8_grouped_kernel(const i8_proble
   }
   const int* prefix = sched + kSchedHdr;
   const int* entry = prefix + ne + 1;
-  int lo = 0, hi = ne - 1;   // largest e with prefix[e] <= tile
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (prefix[mid] <= tile) lo = mid; else hi = mid - 1;
+  const int per = sched[2];   // tiles of every entry when they are all equal (no search), else 0
+  int lo;
+  if (per > 0) {
+    lo = tile / per;
+  } else {
+    lo = 0;                   // largest e with prefix[e] <= tile
+    int hi = ne - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (prefix[mid] <= tile) lo = mid; else hi = mid - 1;
+    }
   }
   const int e = entry[lo];
-  const int cfg = e & 3, pi = e >> 2;
-  const int local = tile - prefix[lo];
-  const i8_problem P = probs[pi];
-  I8Epi epi{0u, 1u, 0u, 0u};
-  if (epis) epi = epis[pi];
-  const int bm = i8_tile_m(cfg), bn = i8_tile_n(cfg);
-  const int tiles_m = (P.m + bm - 1) / bm, tiles_n = (P.n + bn - 1) / bn;
-  // grouped raster: blocks of kGroupM tile-rows, m fastest inside a block
-  const int per_group = kGroupM * tiles_n;
+  return TileRef{e >> 2, e & 3, tile - (per > 0 ? lo * per : prefix[lo])};
+}
+// grouped raster inside a product: blocks of kGroupM tile-rows, m fastest inside a block
+__device__ __forceinline__ void raster(int local, int m, int n, int bm, int bn, int& tm, int& tn) {
+  const int tiles_m = (m + bm - 1) / bm, tiles_n = (n + bn - 1) / bn;
+  const int per_group = kGroupM * tiles_n;   // blocks of kGroupM tile-rows, m fastest inside a block
   const int g = local / per_group, first_m = g * kGroupM;
   const int gsz = min(kGroupM, tiles_m - first_m);
   const int r = local - g * per_group;
-  const int tm = first_m + r % gsz, tn = r / gsz;
-  switch (cfg) {
+  tm = first_m + r % gsz;
+  tn = r / gsz;
+}
+
+__global__ void __launch_bounds__(kThreads, 2) i8_grouped_kernel(const i8_problem* __restrict__ probs,
+                                                                 const I8Epi* __restrict__ epis,
+                                                                 const int* __restrict__ sched) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+  const TileRef t = find_tile(sched);
+  const i8_problem P = probs[t.pi];
+  I8Epi epi{0u, 1u, 0u, 0u};
+  if (epis) epi = epis[t.pi];
+  int tm, tn;
+  raster(t.local, P.m, P.n, i8_tile_m(t.cfg), i8_tile_n(t.cfg), tm, tn);
+  switch (t.cfg) {
     case 0: run_tile<Cfg0>(lds, P, epi, tm, tn); break;
     case 1: run_tile<Cfg1>(lds, P, epi, tm, tn); break;
     default: run_tile<Cfg2>(lds, P, epi, tm, tn); break;
   }
+}
+
+// every tile of the schedule is a 256 x 256 tile
+__global__ void __launch_bounds__(kThreadsL, 1) i8_large_kernel(const i8_problem* __restrict__ probs,
+                                                                const I8Epi* __restrict__ epis,
+                                                                const int* __restrict__ sched) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+  const TileRef t = find_tile(sched);
+  const i8_problem P = probs[t.pi];
+  I8Epi epi{0u, 1u, 0u, 0u};
+  if (epis) epi = epis[t.pi];
+  int tm, tn;
+  raster(t.local, P.m, P.n, CfgL::BM, CfgL::BN, tm, tn);
+  run_tile<CfgL>(lds, P, epi, tm, tn);
 }
 
 // ----------------------------------------------------------------------------- host side
@@ -292,9 +338,11 @@ int auto_cfg(int m, int n) {
 
 }  // namespace
 
-int i8_build_schedule(const i8_problem* h, int num, void* h_ws, size_t ws_bytes, i8_sched_info* info, int num_cus) {
+int i8_build_schedule(const i8_problem* h, int num, void* h_ws, size_t ws_bytes, i8_sched_info* info, int num_cus,
+                      int allow_large, int* kernel) {
   if (num < 0 || (num > 0 && !h) || !h_ws || !info) return 1;
   if (ws_bytes < sched_bytes(num)) return 2;
+  if (kernel) *kernel = kI8General;
   std::lock_guard<std::mutex> lk(g_mu);
   std::vector<Ent>& ents = g_ents;
   ents.clear();
@@ -319,6 +367,23 @@ int i8_build_schedule(const i8_problem* h, int num, void* h_ws, size_t ws_bytes,
         e.cost = (double)i8_tile_m(e.cfg) * i8_tile_n(e.cfg) * (double)(h[e.prob].kp + 128);
       }
   }
+  // large-tile kernel: every product on automatic large tiles, and enough 256 x 256 tiles to give
+  // every compute unit one
+  if (allow_large && !ents.empty()) {
+    bool all = true;
+    long long t = 0;
+    for (auto& e : ents) {
+      all = all && e.cfg == 0 && h[e.prob].tile_cfg < 0;
+      t += (long long)((h[e.prob].m + 255) / 256) * ((h[e.prob].n + 255) / 256);
+    }
+    if (all && t >= num_cus) {
+      for (auto& e : ents) {
+        e.tiles = ((h[e.prob].m + 255) / 256) * ((h[e.prob].n + 255) / 256);
+        e.cost = 256.0 * 256.0 * (double)(h[e.prob].kp + 128);
+      }
+      if (kernel) *kernel = kI8Large;
+    }
+  }
   std::stable_sort(ents.begin(), ents.end(), [](const Ent& a, const Ent& b) {
     if (a.cost != b.cost) return a.cost > b.cost;
     return a.tiles > b.tiles;
@@ -338,6 +403,9 @@ int i8_build_schedule(const i8_problem* h, int num, void* h_ws, size_t ws_bytes,
   std::memset(img, 0, sizeof(int) * kSchedHdr);
   img[0] = (int)tot;
   img[1] = (int)ne;
+  bool same = ne > 0;
+  for (size_t j = 1; j < ne && same; ++j) same = ents[j].tiles == ents[0].tiles;
+  img[2] = same ? ents[0].tiles : 0;
   info->tiles_main = (int)tot;
   info->tiles_splitk = 0;
   info->num_launches = tot > 0 ? 1 : 0;
@@ -346,28 +414,43 @@ int i8_build_schedule(const i8_problem* h, int num, void* h_ws, size_t ws_bytes,
   return 0;
 }
 
+I8Epi i8_epi_residue(uint32_t p) {
+  return I8Epi{1u, p, (uint32_t)((4294967296ull + p - 1) / p), p * (uint32_t)((2147483648ull + p - 1) / p)};
+}
+
+namespace {
+// the kernels' dynamic LDS exceeds the default limit: raise it once per device
+bool lds_attrs_set() {
+  static std::mutex mu;
+  static std::vector<int> done;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return false;
+  std::lock_guard<std::mutex> lk(mu);
+  if ((int)done.size() <= dev) done.resize(dev + 1, 0);
+  if (!done[dev]) {
+    if (hipFuncSetAttribute((const void*)i8_grouped_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kSmem) !=
+            hipSuccess ||
+        hipFuncSetAttribute((const void*)i8_large_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kSmemL) !=
+            hipSuccess)
+      return false;
+    done[dev] = 1;
+  }
+  return true;
+}
+}  // namespace
+
 int i8_launch(const i8_problem* d_probs, const I8Epi* d_epi, const void* d_sched, const i8_sched_info* info,
-              hipStream_t s) {
+              hipStream_t s, int kernel) {
   if (!info) return 1;
   if (info->num_launches == 0 || info->tiles_main == 0) return 0;
   if (!d_probs || !d_sched) return 1;
-  // 72 KB of dynamic LDS exceeds the default limit: raise it once per device
-  static std::mutex attr_mu;
-  static std::vector<int> attr_done;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 6;
-  {
-    std::lock_guard<std::mutex> lk(attr_mu);
-    if ((int)attr_done.size() <= dev) attr_done.resize(dev + 1, 0);
-    if (!attr_done[dev]) {
-      if (hipFuncSetAttribute((const void*)i8_grouped_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kSmem) !=
-          hipSuccess)
-        return 6;
-      attr_done[dev] = 1;
-    }
-  }
-  hipLaunchKernelGGL(i8_grouped_kernel, dim3((unsigned)info->tiles_main), dim3(kThreads), kSmem, s, d_probs, d_epi,
-                     static_cast<const int*>(d_sched));
+  if (!lds_attrs_set()) return 6;
+  if (kernel == kI8Large)
+    hipLaunchKernelGGL(i8_large_kernel, dim3((unsigned)info->tiles_main), dim3(kThreadsL), kSmemL, s, d_probs, d_epi,
+                       static_cast<const int*>(d_sched));
+  else
+    hipLaunchKernelGGL(i8_grouped_kernel, dim3((unsigned)info->tiles_main), dim3(kThreads), kSmem, s, d_probs, d_epi,
+                       static_cast<const int*>(d_sched));
   return hipGetLastError() == hipSuccess ? 0 : 6;
 }
 

@@ -174,6 +174,17 @@ def test_uniform_group_beta(path):
     check_case(case, path, cfg, st, O.REPAIR_ON if path == G.PATH_AUTO else O.REPAIR_COUNT)
 
 
+def test_large_tile_kernel_ragged_edges():
+    """Every product on automatic large tiles and enough 256 x 256 tiles to fill the GPU: the
+    pipeline takes the large-tile INT8 kernel.  m, n are not multiples of 256 (clamped edge rows)
+    and kp = 480 is 32 mod 64 (the zeroed half stage)."""
+    case = Case([(520, 600, 470)] * 3, 20261206, phi=0.5, beta=0.5)
+    say("large-tile kernel, ragged edges")
+    rc, st = run(case, G.PATH_EMU_GROUPED, CFG_EMU)
+    assert rc == 0
+    check_case(case, G.PATH_EMU_GROUPED, CFG_EMU, st, O.REPAIR_COUNT)
+
+
 def test_ragged_group_auto():
     """Config-3 family, reduced: m, n log-uniform in [16, 300], k log-uniform in [1, 700] (k <= 16
     takes SMALL_K, k in (16, 32) exercises Kp padding), alpha ~ U(-2, 2) with 3 zeros,
