@@ -1,6 +1,7 @@
 // call.hpp -- descriptor building and launch sequencing shared by direct calls and plans.
 #pragma once
 #include "common.hpp"
+#include "ggemm_reuse.h"
 
 namespace ggemm {
 
@@ -9,9 +10,10 @@ namespace ggemm {
 //   [F64 schedule(s)][INT8 schedule(s)]
 // every section 256-byte aligned; the INT8 schedule is last so the H2D can stop at its used size.
 struct BlobLayout {
-  size_t off_oz, off_yd, off_i8, off_epi, off_f64, off_sf64, off_si8, total;
+  size_t off_oz, off_yd, off_prep, off_i8, off_epi, off_f64, off_sf64, off_si8, total;
 };
-BlobLayout layout_for(size_t ne, size_t n_i8, size_t nn, size_t sched_f64, size_t sched_i8);
+// nprep: prep descriptors of operand reuse (unique A, then unique B), 0 without reuse
+BlobLayout layout_for(size_t ne, size_t nprep, size_t n_i8, size_t nn, size_t sched_f64, size_t sched_i8);
 inline size_t sched_img(int entries) { return align_up(sched_bytes(entries), kBufAlign); }
 
 // Everything the launch sequence of one grouped call needs.
@@ -19,6 +21,8 @@ struct GroupedCall {
   int ne = 0, nn = 0;             // emulated / native problems
   size_t n_i8 = 0;                // (problem, plane) INT8 products
   int max_m = 0, max_n = 0;
+  int nprep = 0;                  // operand reuse: prep descriptors (0: prep runs on the ne problems)
+  int pmax_m = 0, pmax_n = 0;     // prep grid over the unique operands
   BlobLayout L{};
   i8_sched_info i8info{};
   int i8_kernel = kI8General;     // INT8 GEMM kernel the schedule was built for
@@ -34,8 +38,10 @@ int counters_read(ggemm_handle_t h, hipStream_t s, ggemm_stats_t* st);
 // Plans nothing: takes the planner output and fills descriptors + schedules into hb (capacity
 // cap), and the stats fields num_fallback / moduli_* / reuse_* / num_unique_*.  emu_idx and
 // nat_idx are caller scratch of >= num ints.  Returns GGEMM_OK, WORKSPACE, INVALID or I8GEMM.
+// rp: operand-reuse plan (path EMU_GROUPED_REUSE) or nullptr
 int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const ggemm_plan_entry_t* plan,
-                  int* emu_idx, int* nat_idx, char* hb, size_t cap, GroupedCall* out, ggemm_stats_t* st);
+                  int* emu_idx, int* nat_idx, char* hb, size_t cap, GroupedCall* out, ggemm_stats_t* st,
+                  const reuse_plan* rp = nullptr);
 // Enqueues prep -> INT8 GEMM -> reconstruct (if ne > 0) and the native FP64 GEMM (if nn > 0) on s,
 // reading descriptors from the device blob db.  *launches += kernels issued.  prof_set: stage
 // timing event set (-1 = none).

@@ -148,4 +148,10 @@ struct ggemm_handle_s {
   ggemm_device_model_t dm;
   int ws_diag_printed;
   int stats_repair;
+
+  // operand reuse (path EMU_GROUPED_REUSE): host pass storage and per-unique-operand offsets
+  struct reuse_arena_s* reuse;
+  int* reuse_nmod;
+  size_t *ua_off8, *ua_offs, *ub_off8, *ub_offs;
+  int reuse_promote;   // GGEMM_REUSE_PROMOTE=1 at create: PROMOTE policy, else EXACT_N
 };

@@ -55,11 +55,12 @@ void mark(int s, int q, hipStream_t st) {
 }
 }  // namespace prof
 
-BlobLayout layout_for(size_t ne, size_t n_i8, size_t nn, size_t sched_f64, size_t sched_i8) {
+BlobLayout layout_for(size_t ne, size_t nprep, size_t n_i8, size_t nn, size_t sched_f64, size_t sched_i8) {
   BlobLayout L;
   L.off_oz = 0;
   L.off_yd = align_up(ne * sizeof(oz2_problem), kBufAlign);
-  L.off_i8 = align_up(L.off_yd + ne * sizeof(YDesc), kBufAlign);
+  L.off_prep = align_up(L.off_yd + ne * sizeof(YDesc), kBufAlign);
+  L.off_i8 = align_up(L.off_prep + nprep * sizeof(oz2_problem), kBufAlign);
   L.off_epi = align_up(L.off_i8 + n_i8 * sizeof(i8_problem), kBufAlign);
   L.off_f64 = align_up(L.off_epi + n_i8 * sizeof(I8Epi), kBufAlign);
   L.off_sf64 = align_up(L.off_f64 + nn * sizeof(F64Problem), kBufAlign);
@@ -128,7 +129,8 @@ static void workspace_diag(ggemm_handle_t h, const ggemm_problem_t* probs, const
 }
 
 int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const ggemm_plan_entry_t* plan,
-                  int* emu_idx, int* nat_idx, char* hb, size_t cap, GroupedCall* out, ggemm_stats_t* st) {
+                  int* emu_idx, int* nat_idx, char* hb, size_t cap, GroupedCall* out, ggemm_stats_t* st,
+                  const reuse_plan* rp) {
   GroupedCall c;
   int nmax = 0, pmax = 0;
   size_t SA = 0, SB = 0, SC = 0, rows = 0, cols = 0;
@@ -139,15 +141,39 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
     const ggemm_problem_t& p = probs[g];
     const size_t kp = (size_t)kp_of(p.k);
     emu_idx[c.ne++] = g;
-    SA += align_up((size_t)p.m * kp, kBufAlign);
-    SB += align_up((size_t)p.n * kp, kBufAlign);
+    if (!rp) {   // every emulated problem owns its residue and shift blocks
+      SA += align_up((size_t)p.m * kp, kBufAlign);
+      SB += align_up((size_t)p.n * kp, kBufAlign);
+      rows += align_up((size_t)OZ2_ROW_WS_PER_ROW * p.m, 64);
+      cols += align_up((size_t)OZ2_ROW_WS_PER_ROW * p.n, 64);
+    }
     SC += align_up((size_t)p.m * p.n, kBufAlign / 4);
-    rows += align_up((size_t)OZ2_ROW_WS_PER_ROW * p.m, 64);
-    cols += align_up((size_t)OZ2_ROW_WS_PER_ROW * p.n, 64);
     const int planes = e.num_moduli + OZ2_EXTRA_PLANES;
     c.n_i8 += planes;
     nmax = std::max(nmax, e.num_moduli);
     pmax = std::max(pmax, planes);
+  }
+  if (rp) {   // residue and shift blocks per unique operand (src/ggemm.cu:428-449)
+    for (int u = 0; u < rp->num_ua; ++u) {
+      const ggemm_problem_t& p = probs[rp->ua_rep[u]];
+      h->ua_off8[u] = SA;
+      h->ua_offs[u] = rows;
+      SA += align_up((size_t)p.m * kp_of(p.k), kBufAlign);
+      rows += align_up((size_t)OZ2_ROW_WS_PER_ROW * p.m, 64);
+      pmax = std::max(pmax, rp->ua_nmod[u] + OZ2_EXTRA_PLANES);
+      c.pmax_m = std::max(c.pmax_m, p.m);
+    }
+    for (int u = 0; u < rp->num_ub; ++u) {
+      const ggemm_problem_t& p = probs[rp->ub_rep[u]];
+      h->ub_off8[u] = SB;
+      h->ub_offs[u] = cols;
+      SB += align_up((size_t)p.n * kp_of(p.k), kBufAlign);
+      cols += align_up((size_t)OZ2_ROW_WS_PER_ROW * p.n, 64);
+      pmax = std::max(pmax, rp->ub_nmod[u] + OZ2_EXTRA_PLANES);
+      c.pmax_n = std::max(c.pmax_n, p.n);
+    }
+    c.nprep = rp->num_ua + rp->num_ub;
+    if (c.nprep > 65535) return GGEMM_ERR_INVALID;
   }
   if ((size_t)pmax * SA > h->A8_bytes || (size_t)pmax * SB > h->B8_bytes ||
       (size_t)pmax * SC * sizeof(int32_t) > h->C32_bytes || rows > h->row_shift_elems || cols > h->col_shift_elems) {
@@ -165,13 +191,14 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
   st->moduli_min = c.ne ? GGEMM_MAX_MODULI : 0;
   st->moduli_max = nmax;
   for (int j = 0; j < c.ne; ++j) st->moduli_min = std::min(st->moduli_min, plan[emu_idx[j]].num_moduli);
-  st->reuse_enabled = 0;
-  st->num_unique_A = st->num_unique_B = c.ne;
-  st->num_promoted = 0;
+  st->reuse_enabled = rp ? 1 : 0;
+  st->num_unique_A = rp ? rp->num_ua : c.ne;
+  st->num_unique_B = rp ? rp->num_ub : c.ne;
+  st->num_promoted = rp ? rp->num_promoted : 0;
 
   const size_t s_i8 = c.ne ? sched_bytes((int)c.n_i8) : 0;
   const size_t s_f64 = c.nn ? sched_bytes(c.nn) : 0;
-  c.L = layout_for(c.ne, c.n_i8, c.nn, s_f64, s_i8);
+  c.L = layout_for(c.ne, c.nprep, c.n_i8, c.nn, s_f64, s_i8);
   if (c.L.total > cap) return GGEMM_ERR_INVALID;
   oz2_problem* hoz = reinterpret_cast<oz2_problem*>(hb + c.L.off_oz);
   YDesc* hyd = reinterpret_cast<YDesc*>(hb + c.L.off_yd);
@@ -195,9 +222,19 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
     o.m = p.m; o.n = p.n; o.k = p.k; o.kp = (int)kp; o.num_moduli = e.num_moduli;
     o.lda = p.lda; o.ldb = p.ldb; o.ldc = p.ldc;
     o.A = p.A; o.B = p.B; o.C = p.C; o.alpha = p.alpha; o.beta = p.beta;
-    o.A8 = h->A8 + oa; o.a8_mod_stride = SA;
-    o.B8 = h->B8 + ob; o.b8_mod_stride = SB;
-    o.row_shift = h->row_shift + orow; o.col_shift = h->col_shift + ocol;
+    if (rp) {
+      // the shared operands were prepped with their unique operand's N: it must be this problem's
+      const int ua = rp->prob_a[g], ub = rp->prob_b[g];
+      if (ua < 0 || ub < 0 || rp->ua_nmod[ua] != e.num_moduli || rp->ub_nmod[ub] != e.num_moduli)
+        return GGEMM_ERR_NUMERICS;
+      o.A8 = h->A8 + h->ua_off8[ua]; o.row_shift = h->row_shift + h->ua_offs[ua];
+      o.B8 = h->B8 + h->ub_off8[ub]; o.col_shift = h->col_shift + h->ub_offs[ub];
+    } else {
+      o.A8 = h->A8 + oa; o.row_shift = h->row_shift + orow;
+      o.B8 = h->B8 + ob; o.col_shift = h->col_shift + ocol;
+    }
+    o.a8_mod_stride = SA;
+    o.b8_mod_stride = SB;
     YDesc& yd = hyd[j];
     yd.Y = ybase + oy;
     yd.y_stride = SY;
@@ -226,6 +263,31 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
     c.max_m = std::max(c.max_m, p.m);
     c.max_n = std::max(c.max_n, p.n);
   }
+  if (rp) {
+    // prep descriptors (src/ggemm.cu:544-569): unique A as A-only problems (n = 0), then unique B
+    // as B-only problems (m = 0); alpha = 1 so the prep runs; N = the operand's moduli count
+    oz2_problem* hpr = reinterpret_cast<oz2_problem*>(hb + c.L.off_prep);
+    for (int u = 0; u < rp->num_ua; ++u) {
+      const ggemm_problem_t& p = probs[rp->ua_rep[u]];
+      oz2_problem& o = hpr[u];
+      std::memset(&o, 0, sizeof o);
+      o.m = p.m; o.n = 0; o.k = p.k; o.kp = kp_of(p.k); o.num_moduli = rp->ua_nmod[u];
+      o.lda = p.lda; o.ldb = p.ldb; o.ldc = std::max(1, p.m);
+      o.A = p.A; o.alpha = 1.0;
+      o.A8 = h->A8 + h->ua_off8[u]; o.a8_mod_stride = SA; o.b8_mod_stride = SB;
+      o.row_shift = h->row_shift + h->ua_offs[u];
+    }
+    for (int u = 0; u < rp->num_ub; ++u) {
+      const ggemm_problem_t& p = probs[rp->ub_rep[u]];
+      oz2_problem& o = hpr[rp->num_ua + u];
+      std::memset(&o, 0, sizeof o);
+      o.m = 0; o.n = p.n; o.k = p.k; o.kp = kp_of(p.k); o.num_moduli = rp->ub_nmod[u];
+      o.lda = 1; o.ldb = p.ldb; o.ldc = 1;
+      o.B = p.B; o.alpha = 1.0;
+      o.B8 = h->B8 + h->ub_off8[u]; o.a8_mod_stride = SA; o.b8_mod_stride = SB;
+      o.col_shift = h->col_shift + h->ub_offs[u];
+    }
+  }
   for (int i = 0; i < c.nn; ++i) hf[i] = f64_of(probs[nat_idx[i]]);
   if (c.nn && f64_build_schedule(hf, c.nn, hb + c.L.off_sf64, s_f64, &c.f64_tiles, nullptr)) return GGEMM_ERR_INVALID;
   if (c.ne && i8_build_schedule(hi8, (int)c.n_i8, hb + c.L.off_si8, s_i8, &c.i8info, h->num_cus, 1, &c.i8_kernel))
@@ -240,7 +302,10 @@ int enqueue_grouped(const GroupedCall& c, const char* db, hipStream_t s, int rep
   const YDesc* dyd = reinterpret_cast<const YDesc*>(db + c.L.off_yd);
   prof::mark(prof_set, 0, s);
   if (c.ne > 0) {
-    if (prep_launch(doz, c.ne, c.max_m, c.max_n, s, 1)) return GGEMM_ERR_NUMERICS;
+    const bool shared = c.nprep > 0;   // operand reuse: prep once per unique operand
+    if (prep_launch(shared ? reinterpret_cast<const oz2_problem*>(db + c.L.off_prep) : doz, shared ? c.nprep : c.ne,
+                    shared ? c.pmax_m : c.max_m, shared ? c.pmax_n : c.max_n, s, 1))
+      return GGEMM_ERR_NUMERICS;
     ++*launches;
     prof::mark(prof_set, 1, s);
     if (i8_launch(reinterpret_cast<const i8_problem*>(db + c.L.off_i8), reinterpret_cast<const I8Epi*>(db + c.L.off_epi),
@@ -305,7 +370,7 @@ int run_native(ggemm_handle_t h, const ggemm_problem_t* probs, const int* idx, i
   char* db = static_cast<char*>(h->d_desc);
   const size_t per = grouped ? sched_img(cnt) : sched_img(1);
   const size_t simg = grouped ? per : per * cnt;
-  const BlobLayout L = layout_for(0, 0, cnt, simg, 0);
+  const BlobLayout L = layout_for(0, 0, 0, cnt, simg, 0);
   F64Problem* hf = reinterpret_cast<F64Problem*>(hb + L.off_f64);
   for (int i = 0; i < cnt; ++i) hf[i] = f64_of(probs[idx[i]]);
   int tiles[1] = {0};
@@ -404,19 +469,33 @@ int path_emu_loop(ggemm_handle_t h, bool batched, const ggemm_problem_t* probs, 
   return r ? r : r2;
 }
 
+// src/ggemm.cu:375-403: REUSE plans like EMU_GROUPED, EMU_LOOP_BATCHED like EMU_LOOP
 int path_emu(ggemm_handle_t h, ggemm_path_t path, const ggemm_config_t* cfg, const ggemm_problem_t* probs, int num,
              ggemm_stats_t* st, int repair) {
-  const ggemm_path_t plan_path = (path == GGEMM_PATH_EMU_LOOP_BATCHED) ? GGEMM_PATH_EMU_LOOP : path;
+  const bool reuse = path == GGEMM_PATH_EMU_GROUPED_REUSE;
+  const ggemm_path_t plan_path = path == GGEMM_PATH_EMU_LOOP_BATCHED ? GGEMM_PATH_EMU_LOOP
+                                 : reuse                            ? GGEMM_PATH_EMU_GROUPED
+                                                                    : path;
   int r = ggemm_plan_ex(probs, num, cfg, plan_path, &h->dm, h->plan, h->plan_memo, h->plan_memo_cap);
   if (r) return r;
   if (path == GGEMM_PATH_EMU_LOOP || path == GGEMM_PATH_EMU_LOOP_BATCHED)
     return path_emu_loop(h, path == GGEMM_PATH_EMU_LOOP_BATCHED, probs, num, st, repair);
+  reuse_plan rp{};
+  if (reuse) {   // after the plan, before any sizing
+    for (int g = 0; g < num; ++g)
+      h->reuse_nmod[g] = h->plan[g].route == GGEMM_ROUTE_EMU ? h->plan[g].num_moduli : 0;
+    rp = build_operand_reuse(h->reuse, probs, num, h->reuse_nmod, h->reuse_promote ? REUSE_PROMOTE : REUSE_EXACT_N);
+    if (rp.status != REUSE_OK) return rp.status == REUSE_ERR_CAPACITY ? GGEMM_ERR_WORKSPACE : GGEMM_ERR_INVALID;
+    if (h->reuse_promote)   // every problem of a sharing component runs with the component's largest N
+      for (int g = 0; g < num; ++g)
+        if (h->plan[g].route == GGEMM_ROUTE_EMU) h->plan[g].num_moduli = rp.eff_nmod[g];
+  }
   int slot;
   if ((r = acquire_slot(h, &slot))) return r;
   char* hb = host_slot(h, slot);
   char* db = static_cast<char*>(h->d_desc);
   GroupedCall c;
-  r = build_grouped(h, probs, num, h->plan, h->emu_idx, h->nat_idx, hb, h->desc_bytes, &c, st);
+  r = build_grouped(h, probs, num, h->plan, h->emu_idx, h->nat_idx, hb, h->desc_bytes, &c, st, reuse ? &rp : nullptr);
   if (!r && c.h2d_bytes && hipMemcpyAsync(db, hb, c.h2d_bytes, hipMemcpyHostToDevice, h->stream) != hipSuccess)
     r = GGEMM_ERR_CUDA;
   if (!r) r = enqueue_grouped(c, db, h->stream, repair, &st->kernel_launches, prof::begin());
@@ -469,6 +548,12 @@ extern "C" void ggemm_destroy(ggemm_handle_t h) {
   delete[] h->emu_idx;
   delete[] h->nat_idx;
   delete[] h->loop_info;
+  reuse_arena_destroy(h->reuse);
+  delete[] h->reuse_nmod;
+  delete[] h->ua_off8;
+  delete[] h->ua_offs;
+  delete[] h->ub_off8;
+  delete[] h->ub_offs;
   ::operator delete(h);
 }
 
@@ -528,7 +613,7 @@ extern "C" int ggemm_create_ex(ggemm_handle_t* out, int max_problems, size_t max
   const size_t n_i8 = P * M;
   const size_t si8 = std::max({sched_img((int)n_i8), n_i8 * sched_img(1), P * sched_img(kMaxPlanes)});
   const size_t sf64 = std::max(sched_img((int)P), P * sched_img(1));
-  const BlobLayout Lw = layout_for(P, n_i8, P, sf64, sched_img((int)n_i8));
+  const BlobLayout Lw = layout_for(P, 2 * P, n_i8, P, sf64, sched_img((int)n_i8));
   h->desc_bytes = align_up(Lw.total + si8 + kBufAlign, kBufAlign);
   HIPA(hipMalloc(&h->d_desc, h->desc_bytes));
   HIPA(hipHostMalloc(&h->h_desc, h->desc_bytes * kSlots, hipHostMallocDefault));
@@ -543,6 +628,16 @@ extern "C" int ggemm_create_ex(ggemm_handle_t* out, int max_problems, size_t max
   h->nat_idx = new (std::nothrow) int[P];
   h->loop_info = new (std::nothrow) i8_sched_info[P * M];
   if (!h->plan || !h->plan_memo || !h->emu_idx || !h->nat_idx || !h->loop_info) FAIL(GGEMM_ERR_ALLOC);
+  // operand reuse: host arena and offset scratch (nothing is allocated inside calls)
+  if (reuse_arena_create(max_problems, &h->reuse) != REUSE_OK) FAIL(h->reuse ? GGEMM_ERR_INVALID : GGEMM_ERR_ALLOC);
+  h->reuse_nmod = new (std::nothrow) int[P];
+  h->ua_off8 = new (std::nothrow) size_t[P];
+  h->ua_offs = new (std::nothrow) size_t[P];
+  h->ub_off8 = new (std::nothrow) size_t[P];
+  h->ub_offs = new (std::nothrow) size_t[P];
+  if (!h->reuse_nmod || !h->ua_off8 || !h->ua_offs || !h->ub_off8 || !h->ub_offs) FAIL(GGEMM_ERR_ALLOC);
+  const char* ep = std::getenv("GGEMM_REUSE_PROMOTE");
+  h->reuse_promote = (ep && std::atoi(ep) == 1) ? 1 : 0;
   const char* e = std::getenv("GGEMM_STATS_REPAIR");
   h->stats_repair = (e && std::atoi(e) == 1) ? 1 : 0;
   if (hipStreamSynchronize(stream) != hipSuccess) FAIL(GGEMM_ERR_CUDA);
@@ -574,13 +669,14 @@ extern "C" int ggemm_grouped_dgemm(ggemm_handle_t h, ggemm_path_t path, const gg
     case GGEMM_PATH_EMU_LOOP:
     case GGEMM_PATH_EMU_GROUPED:
     case GGEMM_PATH_AUTO:
+    case GGEMM_PATH_EMU_GROUPED_REUSE:
     case GGEMM_PATH_EMU_LOOP_BATCHED: {
       if ((r = counters_reset(h, h->stream))) return r;
       r = path_emu(h, path, cfg, problems, num_problems, st, repair);
       if (!r) r = counters_read(h, h->stream, st);
       return r;
     }
-    default:   // GGEMM_PATH_EMU_GROUPED_REUSE: operand reuse is not built yet
+    default:
       return GGEMM_ERR_INVALID;
   }
 }

@@ -69,7 +69,7 @@ int build(ggemm_plan_t p, ggemm_path_t path, const ggemm_config_t* cfg) {
     ++ne;
     n_i8 += e.num_moduli + OZ2_EXTRA_PLANES;
   }
-  const BlobLayout L = layout_for(ne, n_i8, nn, nn ? sched_bytes((int)nn) : 0, ne ? sched_bytes((int)n_i8) : 0);
+  const BlobLayout L = layout_for(ne, 0, n_i8, nn, nn ? sched_bytes((int)nn) : 0, ne ? sched_bytes((int)n_i8) : 0);
   p->blob_bytes = align_up(std::max<size_t>(L.total, 1), kBufAlign);
   HIPC(hipMalloc(&p->d_blob, p->blob_bytes));
   HIPC(hipHostMalloc(&p->h_blob, p->blob_bytes, hipHostMallocDefault));

@@ -84,6 +84,23 @@ class DeviceModel(C.Structure):
                 ("mem_bw", C.c_double), ("tiny_mnk", C.c_double)]
 
 
+class ReusePlan(C.Structure):
+    """include/ggemm_reuse.h reuse_plan (a view into the arena)."""
+    _fields_ = [("status", C.c_int), ("num_problems", C.c_int), ("num_ua", C.c_int), ("num_ub", C.c_int),
+                ("num_emu", C.c_int), ("num_promoted", C.c_int),
+                ("ua_rep", C.POINTER(C.c_int)), ("ua_nmod", C.POINTER(C.c_int)),
+                ("ub_rep", C.POINTER(C.c_int)), ("ub_nmod", C.POINTER(C.c_int)),
+                ("prob_a", C.POINTER(C.c_int)), ("prob_b", C.POINTER(C.c_int)), ("eff_nmod", C.POINTER(C.c_int))]
+
+
+class ReuseBytes(C.Structure):
+    _fields_ = [("prep_read", C.c_double), ("prep_write", C.c_double), ("ws_A8", C.c_double),
+                ("ws_B8", C.c_double)]
+
+
+REUSE_EXACT_N, REUSE_PROMOTE = 0, 1
+REUSE_OK, REUSE_ERR_CAPACITY, REUSE_ERR_INVALID = 0, 1, 2
+
 _P = C.c_void_p
 # (name, restype, argtypes) of every exported C entry point
 SIGNATURES = [
@@ -120,6 +137,12 @@ SIGNATURES = [
     ("ggemm_plan_memo_cap", C.c_size_t, [C.c_int]),
     ("ggemm_profile_enable", C.c_int, [C.c_int]),
     ("ggemm_profile_read", C.c_int, [C.POINTER(C.c_double), C.POINTER(C.c_longlong), C.c_int]),
+    ("reuse_arena_create", C.c_int, [C.c_int, C.POINTER(_P)]),
+    ("reuse_arena_destroy", None, [_P]),
+    ("reuse_arena_capacity", C.c_int, [_P]),
+    ("build_operand_reuse", ReusePlan, [_P, C.POINTER(Problem), C.c_int, C.POINTER(C.c_int), C.c_int]),
+    ("operand_reuse_bytes", None, [C.POINTER(ReusePlan), C.POINTER(Problem), C.POINTER(C.c_int),
+                                   C.POINTER(ReuseBytes), C.POINTER(ReuseBytes)]),
 ]
 
 _lib = None

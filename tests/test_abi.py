@@ -23,7 +23,8 @@ def _declared_functions():
         txt = re.sub(r"//.*", "", txt)
         for m in re.finditer(r"\b([a-z][a-z0-9_]*)\s*\(", txt):
             name = m.group(1)
-            if name.startswith(("ggemm_", "oz2_", "i8_")) and not name.endswith("_t"):
+            if name.startswith(("ggemm_", "oz2_", "i8_", "reuse_arena_", "build_operand_reuse",
+                                "operand_reuse_")) and not name.endswith("_t"):
                 names.add(name)
     return names
 

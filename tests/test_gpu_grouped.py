@@ -233,9 +233,8 @@ def test_edge_cases():
         for path in range(7):
             st = G.Stats()
             rc = G.lib().ggemm_grouped_dgemm(h.h, path, C.byref(CFG_EMU), None, 0, C.byref(st))
-            assert rc == (G.GGEMM_ERR_INVALID if path == G.PATH_EMU_GROUPED_REUSE else 0), path
-            if rc == 0:
-                assert st.num_problems == 0 and st.num_fallback == 0
+            assert rc == 0, path
+            assert st.num_problems == 0 and st.num_fallback == 0 and st.kernel_launches == 0
     cases = [([(100, 70, 50)], 1.0, 0.0), ([(1, 1, 1)], 1.0, 0.0),
              ([(0, 32, 32), (32, 0, 32), (32, 32, 0), (48, 40, 36), (0, 0, 0)], 1.5, -0.5),
              ([(0, 16, 16), (16, 0, 16)], 1.0, 0.0), ([(33, 31, 1), (65, 3, 31), (5, 129, 97)], -2.0, 1.0)]
