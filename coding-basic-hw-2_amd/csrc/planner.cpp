@@ -19,6 +19,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <dlfcn.h>
 
 #include "common.hpp"
 
@@ -92,8 +93,20 @@ void load_calib(const char* gpu_name, double* fp64, double* i8, double* bw, char
   if (env && *env) {
     std::snprintf(path, sizeof path, "%s", env);
   } else {
-    const char* dir = std::getenv("GGEMM_CALIB_DIR");
-    if (!dir || !*dir) return;
+    // GGEMM_CALIB_DIR, else the calib/ directory beside this library's ggemm/ directory (the
+    // reference compiles its calibration directory in, src/planner.cpp:62-78)
+    char dir[1024];
+    const char* env_dir = std::getenv("GGEMM_CALIB_DIR");
+    if (env_dir && *env_dir) {
+      std::snprintf(dir, sizeof dir, "%s", env_dir);
+    } else {
+      Dl_info info;
+      if (!dladdr(reinterpret_cast<void*>(&ggemm_device_model_init), &info) || !info.dli_fname) return;
+      std::snprintf(dir, sizeof dir, "%s", info.dli_fname);
+      char* slash = std::strrchr(dir, '/');
+      if (!slash) return;
+      std::snprintf(slash, sizeof dir - (size_t)(slash - dir), "/../calib");
+    }
     char slug[256];
     slug_of(gpu_name, slug, sizeof slug);
     std::snprintf(path, sizeof path, "%s/params_%s.json", dir, slug);
