@@ -72,15 +72,16 @@ def fill(torch, out, phi, seed, salt, lo_hi=None):
         out.view(-1)[s0:s0 + cnt] = v
 
 
-def measured_traffic(workload):
-    """HBM bytes per INT8 GEMM launch from the committed rocprofv3 counter summary
-    (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by its plain-copy calibration), or None."""
+def measured_traffic(workload, kernel):
+    """HBM bytes per launch of the INT8 GEMM kernel from the committed rocprofv3 counter summary
+    (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by its plain-copy calibration), or None
+    when no summary exists for this workload and kernel."""
     f = REPO / "profiles" / "hbm_traffic.json"
     try:
         rec = json.loads(f.read_text()).get(workload)
     except (OSError, ValueError):
         return None
-    if not rec or rec.get("kernel") != "i8_grouped_kernel":
+    if not rec or rec.get("kernel") != kernel:
         return None
     return rec.get("traffic_bytes")
 
@@ -179,6 +180,7 @@ def main():
     ncalls = C.c_longlong(0)
     G.lib().ggemm_profile_read(stage, C.byref(ncalls), 1)
     G.lib().ggemm_profile_enable(0)
+    i8_kernel = G.lib().ggemm_profile_i8_kernel().decode()
     st_ms = [stage[q] / max(ncalls.value, 1) for q in range(4)]
     i8_ms = st_ms[1]
     achieved = int8_ops / (i8_ms * 1e-3) / 1e12 if i8_ms > 0 else 0.0
@@ -280,9 +282,9 @@ def main():
                      "native": round(st_ms[3], 4)},
         "stage_hbm_gbs": {"prep": round(prep_bytes / (st_ms[0] * 1e-3) / 1e9, 1) if st_ms[0] else None,
                           "reconstruct": round(recon_bytes / (st_ms[2] * 1e-3) / 1e9, 1) if st_ms[2] else None},
-        "roofline": {"bound": "mfma", "kernel": "i8_grouped_kernel", "achieved": round(achieved, 2),
+        "roofline": {"bound": "mfma", "kernel": i8_kernel, "achieved": round(achieved, 2),
                      "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s", "frac": round(achieved / INT8_PEAK_TOPS, 4),
-                     "traffic": measured_traffic(args.workload)},
+                     "traffic": measured_traffic(args.workload, i8_kernel)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))

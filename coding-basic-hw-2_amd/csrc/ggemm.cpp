@@ -28,6 +28,7 @@ int used[kRing];            // marks recorded in the set (0 = free)
 int next = 0;
 double sum_ms[4] = {0, 0, 0, 0};
 long long calls = 0;
+int last_i8 = -1;           // INT8 GEMM kernel of the last grouped call that launched one
 
 void drain(int s) {
   if (!used[s]) return;
@@ -312,6 +313,7 @@ int enqueue_grouped(const GroupedCall& c, const char* db, hipStream_t s, int rep
                   db + c.L.off_si8, &c.i8info, s, c.i8_kernel))
       return GGEMM_ERR_I8GEMM;
     *launches += c.i8info.num_launches;
+    prof::last_i8 = c.i8_kernel;
     prof::mark(prof_set, 2, s);
     if (recon_launch(doz, dyd, c.ne, c.max_m, c.max_n, s, repair)) return GGEMM_ERR_NUMERICS;
     ++*launches;
@@ -529,6 +531,14 @@ extern "C" int ggemm_profile_read(double* ms, long long* n, int reset) {
     calls = 0;
   }
   return GGEMM_OK;
+}
+
+extern "C" const char* ggemm_profile_i8_kernel(void) {
+  switch (ggemm::prof::last_i8) {
+    case ggemm::kI8General: return "i8_grouped_kernel";
+    case ggemm::kI8Large: return "i8_large_kernel";
+    default: return "";
+  }
 }
 
 extern "C" void ggemm_destroy(ggemm_handle_t h) {

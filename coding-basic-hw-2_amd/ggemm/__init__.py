@@ -137,6 +137,7 @@ SIGNATURES = [
     ("ggemm_plan_memo_cap", C.c_size_t, [C.c_int]),
     ("ggemm_profile_enable", C.c_int, [C.c_int]),
     ("ggemm_profile_read", C.c_int, [C.POINTER(C.c_double), C.POINTER(C.c_longlong), C.c_int]),
+    ("ggemm_profile_i8_kernel", C.c_char_p, []),
     ("reuse_arena_create", C.c_int, [C.c_int, C.POINTER(_P)]),
     ("reuse_arena_destroy", None, [_P]),
     ("reuse_arena_capacity", C.c_int, [_P]),

@@ -20,6 +20,9 @@ int ggemm_profile_enable(int on);
  * ms[0] prep, ms[1] INT8 GEMM, ms[2] reconstruct, ms[3] native FP64 GEMM, and the number of
  * calls measured.  reset = 1 clears the sums.  Returns 0 on success. */
 int ggemm_profile_read(double* ms, long long* calls, int reset);
+/* Kernel symbol name of the INT8 GEMM the last grouped call launched ("i8_grouped_kernel" or
+ * "i8_large_kernel", as profilers list it), "" before any.  Recorded whether or not timing is on. */
+const char* ggemm_profile_i8_kernel(void);
 
 #ifdef __cplusplus
 }
