@@ -26,6 +26,7 @@ struct GroupedCall {
   BlobLayout L{};
   i8_sched_info i8info{};
   int i8_kernel = kI8General;     // INT8 GEMM kernel the schedule was built for
+  bool blocked = false;           // digit and abs planes in the blocked layout
   int f64_tiles = 0;
   size_t h2d_bytes = 0;           // bytes of the blob to copy
 };

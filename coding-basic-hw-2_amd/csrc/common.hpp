@@ -78,15 +78,30 @@ inline size_t sched_bytes(int entries) {
 constexpr int kI8NumCfg = 3;
 __host__ __device__ inline int i8_tile_m(int cfg) { return cfg == 0 ? 256 : (cfg == 1 ? 128 : 64); }
 __host__ __device__ inline int i8_tile_n(int cfg) { return cfg == 0 ? 128 : (cfg == 1 ? 128 : 64); }
-// Per-product epilogue of the INT8 GEMM: mode 0 stores the int32 product (C is int32*, ld m);
-// mode 1 stores one byte per entry, the residue C mod p in [0, p), from u = C + bias in [0, 2^32)
-// (bias = p ceil(2^31 / p)) by a Barrett step with mc = ceil(2^32 / p) and one correction.
-// In the production pipeline the A residues of plane l carry the CRT inverse q_l (prep with
-// fold_q), so this byte is the CRT digit y_l = (C_l q_l) mod p_l.
+// Per-product epilogue of the INT8 GEMM, mode bits:
+//   kEpiResidue  one byte per entry, the residue C mod p in [0, p), from u = C + bias in [0, 2^32)
+//                (bias = p ceil(2^31 / p)) by a Barrett step with mc = ceil(2^32 / p) and one
+//                correction; without it the int32 product.  In the production pipeline the A
+//                residues of plane l carry the CRT inverse q_l (prep with fold_q), so this byte
+//                is the CRT digit y_l = (C_l q_l) mod p_l.
+//   kEpiBlocked  16 x 16 blocked output (below) instead of column-major with ld m.
+// Blocked layout of an m x n plane: blocks (bi, bj) of 16 x 16 entries in column-major block
+// order (MB = ceil(m / 16) block rows), each block stored as one MFMA result block: lane
+// l = 16 q + c holds rows 4 q .. 4 q + 3 of column c, i.e. 4 consecutive bytes (digits) or 16
+// bytes (int32) per lane, 256 / 1024 contiguous bytes per block.  Entries beyond m x n inside a
+// block are padding.
+enum : uint32_t { kEpiResidue = 1u, kEpiBlocked = 2u };
 struct I8Epi {
   uint32_t mode, p, mc, bias;
 };
 I8Epi i8_epi_residue(uint32_t p);
+__host__ __device__ inline size_t blocked_plane_entries(int m, int n) {
+  return (size_t)((m + 15) / 16) * (size_t)((n + 15) / 16) * 256;
+}
+// offset in entries of the word holding rows r4 .. r4 + 3 (r4 % 4 == 0) of column c
+__host__ __device__ inline size_t blocked_word(int r4, int c, int mb) {
+  return ((size_t)(c >> 4) * (size_t)mb + (size_t)(r4 >> 4)) * 256 + (size_t)(16 * ((r4 & 15) >> 2) + (c & 15)) * 4;
+}
 // INT8 GEMM kernels: the general one (tile configs 0..2, two workgroups per compute unit) and the
 // large-tile one (every tile 256 x 256, one 8-wave workgroup per compute unit).
 enum { kI8General = 0, kI8Large = 1 };
@@ -100,7 +115,8 @@ int i8_launch(const i8_problem* d_probs, const I8Epi* d_epi, const void* d_sched
               hipStream_t s, int kernel = kI8General);
 
 // Where the reconstruct reads a problem's plane products in the production pipeline: CRT digits
-// y_l (one byte per entry, plane l at Y + l * y_stride, ld m) and the abs-plane product L (int32).
+// y_l (one byte per entry, plane l at Y + l * y_stride) and the abs-plane product L (int32), both
+// column-major with ld m, or both blocked (layout above) when the call's descriptors say so.
 struct YDesc {
   const uint8_t* Y;
   size_t y_stride;
@@ -117,7 +133,9 @@ int f64_launch(const F64Problem* d_probs, const void* d_sched, int total_tiles, 
 // CRT inverse of modulus l for the problem's N; the abs plane and B are unchanged.
 int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t s, int fold_q = 0);
 // yd == nullptr: read the int32 planes of oz2_problem::C32 (kernel-level API); else the digits.
-int recon_launch(const oz2_problem* d, const YDesc* yd, int num, int max_m, int max_n, hipStream_t s, int mode);
+// blocked: the digits and L of every problem are in the blocked layout (production, yd != nullptr)
+int recon_launch(const oz2_problem* d, const YDesc* yd, int num, int max_m, int max_n, hipStream_t s, int mode,
+                 bool blocked = false);
 
 }  // namespace ggemm
 
@@ -154,4 +172,5 @@ struct ggemm_handle_s {
   int* reuse_nmod;
   size_t *ua_off8, *ua_offs, *ub_off8, *ub_offs;
   int reuse_promote;   // GGEMM_REUSE_PROMOTE=1 at create: PROMOTE policy, else EXACT_N
+  int digits_colmajor; // GGEMM_DIGITS_COLMAJOR=1 at create: never the blocked digit layout (testing)
 };

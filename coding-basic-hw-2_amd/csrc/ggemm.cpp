@@ -208,9 +208,17 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
   F64Problem* hf = reinterpret_cast<F64Problem*>(hb + c.L.off_f64);
   const CrtTables* tab = host_tables();
   // product workspace (the C32 buffer): CRT digit planes [plane < nmax][problem] of SY bytes
-  // each, then the int32 abs-plane products; fits because nmax SY + 4 SC <= pmax 4 SC.
-  size_t SY = 0;
-  for (int j = 0; j < c.ne; ++j) SY += align_up((size_t)probs[emu_idx[j]].m * probs[emu_idx[j]].n, kBufAlign);
+  // each, then the int32 abs-plane products.  Column-major fits because nmax SY + 4 SC <=
+  // pmax 4 SC; the blocked layout (whole 16 x 16 blocks) is used when its padded planes fit too.
+  size_t SY = 0, SYb = 0, SLb = 0;
+  for (int j = 0; j < c.ne; ++j) {
+    const ggemm_problem_t& p = probs[emu_idx[j]];
+    SY += align_up((size_t)p.m * p.n, kBufAlign);
+    SYb += align_up(blocked_plane_entries(p.m, p.n), kBufAlign);
+    SLb += align_up(blocked_plane_entries(p.m, p.n), kBufAlign / 4) * sizeof(int32_t);
+  }
+  c.blocked = !h->digits_colmajor && (size_t)nmax * SYb + SLb <= h->C32_bytes;
+  if (c.blocked) SY = SYb;
   uint8_t* ybase = reinterpret_cast<uint8_t*>(h->C32);
   int32_t* lbase = reinterpret_cast<int32_t*>(ybase + (size_t)nmax * SY);
   size_t oa = 0, ob = 0, orow = 0, ocol = 0, q = 0, oy = 0, ol = 0;
@@ -254,9 +262,11 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
         d.C = lbase + ol;
         hepi[q] = I8Epi{0u, 1u, 0u, 0u};
       }
+      if (c.blocked) hepi[q].mode |= kEpiBlocked;
     }
-    oy += align_up((size_t)p.m * p.n, kBufAlign);
-    ol += align_up((size_t)p.m * p.n, kBufAlign / 4);
+    const size_t plane = c.blocked ? blocked_plane_entries(p.m, p.n) : (size_t)p.m * p.n;
+    oy += align_up(plane, kBufAlign);
+    ol += align_up(plane, kBufAlign / 4);
     oa += align_up((size_t)p.m * kp, kBufAlign);
     ob += align_up((size_t)p.n * kp, kBufAlign);
     orow += align_up((size_t)OZ2_ROW_WS_PER_ROW * p.m, 64);
@@ -315,7 +325,7 @@ int enqueue_grouped(const GroupedCall& c, const char* db, hipStream_t s, int rep
     *launches += c.i8info.num_launches;
     prof::last_i8 = c.i8_kernel;
     prof::mark(prof_set, 2, s);
-    if (recon_launch(doz, dyd, c.ne, c.max_m, c.max_n, s, repair)) return GGEMM_ERR_NUMERICS;
+    if (recon_launch(doz, dyd, c.ne, c.max_m, c.max_n, s, repair, c.blocked)) return GGEMM_ERR_NUMERICS;
     ++*launches;
     prof::mark(prof_set, 3, s);
   } else {
@@ -458,7 +468,10 @@ int path_emu_loop(ggemm_handle_t h, bool batched, const ggemm_problem_t* probs, 
       if (r) break;
     }
     q += planes;
-    if (recon_launch(doz + j, dyd + j, 1, hoz[j].m, hoz[j].n, h->stream, repair)) { r = GGEMM_ERR_NUMERICS; break; }
+    if (recon_launch(doz + j, dyd + j, 1, hoz[j].m, hoz[j].n, h->stream, repair, c.blocked)) {
+      r = GGEMM_ERR_NUMERICS;
+      break;
+    }
     ++nl;
   }
   if (!r && c.nn > 0 && c.f64_tiles > 0) {
@@ -648,6 +661,8 @@ extern "C" int ggemm_create_ex(ggemm_handle_t* out, int max_problems, size_t max
   if (!h->reuse_nmod || !h->ua_off8 || !h->ua_offs || !h->ub_off8 || !h->ub_offs) FAIL(GGEMM_ERR_ALLOC);
   const char* ep = std::getenv("GGEMM_REUSE_PROMOTE");
   h->reuse_promote = (ep && std::atoi(ep) == 1) ? 1 : 0;
+  const char* ec = std::getenv("GGEMM_DIGITS_COLMAJOR");
+  h->digits_colmajor = (ec && std::atoi(ec) == 1) ? 1 : 0;
   const char* e = std::getenv("GGEMM_STATS_REPAIR");
   h->stats_repair = (e && std::atoi(e) == 1) ? 1 : 0;
   if (hipStreamSynchronize(stream) != hipSuccess) FAIL(GGEMM_ERR_CUDA);

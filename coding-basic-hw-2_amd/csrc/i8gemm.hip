@@ -30,6 +30,8 @@
 // Epilogue, per problem: int32 C (the reference contract, used by the kernel-level API and the
 // abs plane), or -- in the production pipeline -- one residue byte C mod p per entry (I8Epi),
 // which with q-folded A residues is the CRT digit; this cuts the plane write from 4 to 1 byte.
+// The production pipeline also stores in the blocked layout: each 16 x 16 MFMA result block is one
+// contiguous 256-byte (digits) or 1 KB (int32) store instead of 16 column pieces.
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -194,9 +196,32 @@ __device__ __forceinline__ void run_tile(uint8_t* lds, const i8_problem& P, cons
   }
 
   // D block layout: lane l, register r -> row 4 (l / 16) + r, column l % 16; a lane's 4 values
-  // are 4 consecutive rows of one column, i.e. contiguous in the column-major output.
+  // are 4 consecutive rows of one column, i.e. contiguous in the column-major output, and the
+  // 64 lanes' values are one 16 x 16 block of the blocked output layout.
+  const bool residue = (epi.mode & kEpiResidue) != 0;
+  if (epi.mode & kEpiBlocked) {   // every existing block is stored whole (padding included)
+    const int mb = (P.m + 15) / 16;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int br = row0 + wm * C::WM + i * 16, bc = col0 + wn * C::WN + j * 16;
+        if (br >= P.m || bc >= P.n) continue;
+        const size_t w = blocked_word(br + 4 * (lane >> 4), bc + (lane & 15), mb);
+        const v4i v = acc[i][j];
+        if (residue) {
+          uint32_t y[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) y[r] = residue_byte(v[r], epi);
+          *reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(P.C) + w) = y[0] | (y[1] << 8) | (y[2] << 16) | (y[3] << 24);
+        } else {
+          *reinterpret_cast<v4i*>(reinterpret_cast<int32_t*>(P.C) + w) = v;
+        }
+      }
+    return;
+  }
   const size_t ldc = (size_t)P.m;
-  const bool vec = (P.m % 4 == 0) && ((reinterpret_cast<uintptr_t>(P.C) & (epi.mode ? 3 : 15)) == 0);
+  const bool vec = (P.m % 4 == 0) && ((reinterpret_cast<uintptr_t>(P.C) & (residue ? 3 : 15)) == 0);
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -205,7 +230,7 @@ __device__ __forceinline__ void run_tile(uint8_t* lds, const i8_problem& P, cons
       const int r0 = row0 + wm * C::WM + i * 16 + 4 * (lane >> 4);
       if (col >= P.n || r0 >= P.m) continue;
       const v4i v = acc[i][j];
-      if (epi.mode == 0) {
+      if (!residue) {
         int32_t* out = reinterpret_cast<int32_t*>(P.C) + (size_t)r0 + (size_t)col * ldc;
         if (vec && r0 + 3 < P.m) {
           *reinterpret_cast<v4i*>(out) = v;
@@ -415,7 +440,7 @@ int i8_build_schedule(const i8_problem* h, int num, void* h_ws, size_t ws_bytes,
 }
 
 I8Epi i8_epi_residue(uint32_t p) {
-  return I8Epi{1u, p, (uint32_t)((4294967296ull + p - 1) / p), p * (uint32_t)((2147483648ull + p - 1) / p)};
+  return I8Epi{kEpiResidue, p, (uint32_t)((4294967296ull + p - 1) / p), p * (uint32_t)((2147483648ull + p - 1) / p)};
 }
 
 namespace {

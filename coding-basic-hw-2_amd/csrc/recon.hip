@@ -15,8 +15,10 @@
 // plane, written by the INT8 GEMM epilogue) and the int32 abs-plane product L; the kernel-level
 // API hands over the int32 plane products C_l and the digits are formed here.  Both give the same
 // y_l, hence the same output bits.
-// Mapping: a workgroup covers 128 rows x 8 columns of one problem; a thread owns 4 consecutive rows
-// of one column, so every per-plane digit read is one 32-bit load, L one 128-bit load, the row
+// Mapping: a workgroup covers 128 rows x 8 columns of one problem (blocked digits: four 16 x 16
+// blocks, one per wave, lane = the block's MFMA lane, so a wave's per-plane digit read is one
+// contiguous 256-byte block); a thread owns 4 consecutive rows of one column, so every per-plane
+// digit read is one 32-bit load, L one 128-bit load, the row
 // words (shift, sigma, norm bounds) four 128-bit loads and C0 two 128-bit loads (m % 4 == 0 and
 // aligned operands; element-wise loads otherwise).  All loads are issued before the arithmetic and
 // go through global-address-space pointers; the CRT constants are scalar.
@@ -37,6 +39,7 @@ typedef double v2d __attribute__((ext_vector_type(2)));
 
 constexpr int kThreads = 256;
 constexpr int kTileM = 128, kTileN = 8;   // rows x columns per workgroup (32 row quads x 8 columns)
+constexpr int kBTileM = 64, kBTileN = 16;  // blocked layout: four 16 x 16 blocks stacked per workgroup
 
 #define GLOBAL __attribute__((address_space(1)))
 template <class T>
@@ -124,7 +127,7 @@ __device__ __forceinline__ double entry(const oz2_problem& pr, const CrtTables* 
   return (beta == 0.0) ? alpha * d : fma(alpha, d, beta * c0);
 }
 
-template <bool kDigits>
+template <bool kDigits, bool kBlocked>
 __global__ void __launch_bounds__(kThreads) recon_kernel(const oz2_problem* __restrict__ probs,
                                                          const YDesc* __restrict__ yds, int mode,
                                                          const CrtTables* __restrict__ tab,
@@ -134,9 +137,19 @@ __global__ void __launch_bounds__(kThreads) recon_kernel(const oz2_problem* __re
   const int N = pr.num_moduli;
   const int m = pr.m, n = pr.n, K = pr.k;
   Counts cn{0u, 0u, 0u};
-  const int tiles_m = (m + kTileM - 1) / kTileM;
-  const int tm = (int)blockIdx.x % max(tiles_m, 1), tn = (int)blockIdx.x / max(tiles_m, 1);
-  const int i0 = tm * kTileM + 4 * (threadIdx.x & 31), j = tn * kTileN + (threadIdx.x >> 5);
+  int i0, j;
+  if (kBlocked) {   // a wave per 16 x 16 block, lane = the block's MFMA lane: 4 rows of one column
+    const int tiles_m = (m + kBTileM - 1) / kBTileM;
+    const int tm = (int)blockIdx.x % max(tiles_m, 1), tn = (int)blockIdx.x / max(tiles_m, 1);
+    const int lane = threadIdx.x & 63;
+    i0 = tm * kBTileM + 16 * (threadIdx.x >> 6) + 4 * (lane >> 4);
+    j = tn * kBTileN + (lane & 15);
+  } else {
+    const int tiles_m = (m + kTileM - 1) / kTileM;
+    const int tm = (int)blockIdx.x % max(tiles_m, 1), tn = (int)blockIdx.x / max(tiles_m, 1);
+    i0 = tm * kTileM + 4 * (threadIdx.x & 31);
+    j = tn * kTileN + (threadIdx.x >> 5);
+  }
   const bool active = N >= 1 && N <= kMaxModuli && m > 0 && n > 0 && i0 < m && j < n;
   if (active) {
     const double alpha = pr.alpha, beta = pr.beta;
@@ -176,7 +189,8 @@ __global__ void __launch_bounds__(kThreads) recon_kernel(const oz2_problem* __re
         }
       }
       csh = cs[j]; tau = cs[n + j]; dbb = cs[2 * n + j]; nbb = cs[3 * n + j];
-      const size_t off = (size_t)i0 + (size_t)j * m;
+      // blocked: the 4-entry word always exists (entries past m are padding, never used)
+      const size_t off = kBlocked ? blocked_word(i0, j, (m + 15) / 16) : (size_t)i0 + (size_t)j * m;
       if (kDigits) {
         const YDesc yd = yds[blockIdx.y];
         const GLOBAL uint8_t* Y = gp(yd.Y) + off;
@@ -184,7 +198,7 @@ __global__ void __launch_bounds__(kThreads) recon_kernel(const oz2_problem* __re
         for (int l = 0; l < kMaxModuli; ++l) {
           if (l < N) {
             const GLOBAL uint8_t* y = Y + (size_t)l * yd.y_stride;
-            if (full) {
+            if (kBlocked || full) {
               yv[l] = *reinterpret_cast<const GLOBAL uint32_t*>(y);
             } else {
               uint32_t v = 0;
@@ -194,7 +208,7 @@ __global__ void __launch_bounds__(kThreads) recon_kernel(const oz2_problem* __re
           }
         }
         const GLOBAL int32_t* L = gp(yd.L) + off;
-        if (full) {
+        if (kBlocked || full) {
           const v4i a = *reinterpret_cast<const GLOBAL v4i*>(L);
           Lv[0] = a.x; Lv[1] = a.y; Lv[2] = a.z; Lv[3] = a.w;
         } else {
@@ -276,7 +290,8 @@ __global__ void __launch_bounds__(kThreads) recon_kernel(const oz2_problem* __re
 
 }  // namespace
 
-int recon_launch(const oz2_problem* d, const YDesc* yd, int num, int max_m, int max_n, hipStream_t s, int mode) {
+int recon_launch(const oz2_problem* d, const YDesc* yd, int num, int max_m, int max_n, hipStream_t s, int mode,
+                 bool blocked) {
   if (num <= 0) return 0;
   if (mode != OZ2_REPAIR_OFF && mode != OZ2_REPAIR_COUNT && mode != OZ2_REPAIR_ON) return 1;
   if (num > 65535 || max_m < 0 || max_n < 0) return 1;
@@ -285,14 +300,19 @@ int recon_launch(const oz2_problem* d, const YDesc* yd, int num, int max_m, int 
   const size_t mn = (size_t)max_m * (size_t)max_n;
   if (mn == 0) return 0;
   // tiles of the largest problem; a problem with fewer tiles returns from the surplus workgroups
-  const size_t gx = (size_t)((max_m + kTileM - 1) / kTileM) * (size_t)((max_n + kTileN - 1) / kTileN);
+  const bool blk = blocked && yd;
+  const int tm = blk ? kBTileM : kTileM, tn = blk ? kBTileN : kTileN;
+  const size_t gx = (size_t)((max_m + tm - 1) / tm) * (size_t)((max_n + tn - 1) / tn);
   if (gx > 0x7fffffffu) return 1;
-  if (yd)
-    hipLaunchKernelGGL(recon_kernel<true>, dim3((unsigned)gx, num), dim3(kThreads), 0, s, d, yd, mode, c->tab,
+  if (blk)
+    hipLaunchKernelGGL((recon_kernel<true, true>), dim3((unsigned)gx, num), dim3(kThreads), 0, s, d, yd, mode, c->tab,
                        c->counters);
+  else if (yd)
+    hipLaunchKernelGGL((recon_kernel<true, false>), dim3((unsigned)gx, num), dim3(kThreads), 0, s, d, yd, mode,
+                       c->tab, c->counters);
   else
-    hipLaunchKernelGGL(recon_kernel<false>, dim3((unsigned)gx, num), dim3(kThreads), 0, s, d, nullptr, mode, c->tab,
-                       c->counters);
+    hipLaunchKernelGGL((recon_kernel<false, false>), dim3((unsigned)gx, num), dim3(kThreads), 0, s, d, nullptr, mode,
+                       c->tab, c->counters);
   return hipGetLastError() == hipSuccess ? 0 : 3;
 }
 

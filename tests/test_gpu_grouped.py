@@ -185,6 +185,46 @@ def test_large_tile_kernel_ragged_edges():
     check_case(case, G.PATH_EMU_GROUPED, CFG_EMU, st, O.REPAIR_COUNT)
 
 
+def test_large_tile_kernel_mixed_k_stream():
+    """The large-tile kernel keeps one workgroup per compute unit and streams k-stages across
+    its tiles: products with 1 to 9 k-stages (kp = 64 .. 576, some 32 mod 64) follow each other
+    in one workgroup's ring, with full tiles (exact stores) and a ragged n (edge stores)."""
+    shapes = [(512, 512, 40), (512, 512, 64), (512, 512, 100), (512, 512, 160),
+              (512, 520, 300), (512, 512, 520), (512, 512, 576)]
+    case = Case(shapes, 20261207, phi=0.5, beta=0.5)
+    say("large-tile kernel, mixed k stream")
+    rc, st = run(case, G.PATH_EMU_GROUPED, CFG_EMU)
+    assert rc == 0
+    check_case(case, G.PATH_EMU_GROUPED, CFG_EMU, st, O.REPAIR_COUNT)
+
+
+@pytest.mark.parametrize("shapes", [[(300, 270, 200)] * 2 + [(17, 33, 90), (64, 48, 40)],   # general kernel
+                                    [(520, 600, 470)] * 3],                                   # large-tile kernel
+                         ids=["general", "large"])
+def test_blocked_and_columnmajor_digits_same_bits(shapes):
+    """The CRT digits and abs-plane products travel from the INT8 GEMM to the reconstruct in the
+    blocked 16 x 16 layout when the padded planes fit the workspace, else column-major
+    (GGEMM_DIGITS_COLMAJOR=1 forces it).  Both give the oracle's bits; m, n are not multiples of
+    16, so the blocked planes carry padding."""
+    case = Case(shapes, 20261208, phi=0.5, beta=0.5)
+    say("blocked vs column-major digits")
+    outs = []
+    for colmajor in (False, True):
+        if colmajor:
+            os.environ["GGEMM_DIGITS_COLMAJOR"] = "1"
+        try:
+            h = G.Handle(len(shapes), *case.sizes())
+        finally:
+            os.environ.pop("GGEMM_DIGITS_COLMAJOR", None)
+        with h:
+            rc, st = run(case, G.PATH_EMU_GROUPED, CFG_EMU, handle=h)
+            assert rc == 0
+            check_case(case, G.PATH_EMU_GROUPED, CFG_EMU, st, O.REPAIR_COUNT)
+            outs.append([case.C(g).copy() for g in range(len(shapes))])
+    for a, b in zip(*outs):
+        assert same_bits(a, b)
+
+
 def test_ragged_group_auto():
     """Config-3 family, reduced: m, n log-uniform in [16, 300], k log-uniform in [1, 700] (k <= 16
     takes SMALL_K, k in (16, 32) exercises Kp padding), alpha ~ U(-2, 2) with 3 zeros,
