@@ -27,6 +27,7 @@ struct GroupedCall {
   i8_sched_info i8info{};
   int i8_kernel = kI8General;     // INT8 GEMM kernel the schedule was built for
   bool blocked = false;           // digit and abs planes in the blocked layout
+  bool packed = false;            // residue planes in the packed layout
   int f64_tiles = 0;
   size_t h2d_bytes = 0;           // bytes of the blob to copy
 };

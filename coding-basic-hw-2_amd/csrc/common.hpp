@@ -90,7 +90,18 @@ __host__ __device__ inline int i8_tile_n(int cfg) { return cfg == 0 ? 128 : (cfg
 // l = 16 q + c holds rows 4 q .. 4 q + 3 of column c, i.e. 4 consecutive bytes (digits) or 16
 // bytes (int32) per lane, 256 / 1024 contiguous bytes per block.  Entries beyond m x n inside a
 // block are padding.
-enum : uint32_t { kEpiResidue = 1u, kEpiBlocked = 2u };
+//   kEpiPacked   the residue operands are in the packed layout (below) instead of row-major.
+// Packed layout of a rows x Kp residue plane (production pipeline, same size as row-major): k-blocks
+// of 64 bytes, block b holding the bytes k in [64 b, 64 b + 64) of every row contiguously
+// ([b][row][64]); with Kp % 64 == 32 the last block holds 32 bytes per row.  A 64-byte k-stage of
+// consecutive rows is then one contiguous span.
+enum : uint32_t { kEpiResidue = 1u, kEpiBlocked = 2u, kEpiPacked = 4u };
+constexpr int kPackedMaxKp = 4096;   // production calls whose largest Kp is at most this use packing
+__host__ __device__ inline size_t packed_offset(int row, int k, int rows, int kp) {
+  const int b = k >> 6;
+  const int rb = b == (kp >> 6) ? 32 : 64;
+  return (size_t)b * (size_t)rows * 64 + (size_t)row * rb + (size_t)(k & 63);
+}
 struct I8Epi {
   uint32_t mode, p, mc, bias;
 };
@@ -131,7 +142,8 @@ int f64_launch(const F64Problem* d_probs, const void* d_sched, int total_tiles, 
 // Launchers used by the orchestration (return 0 on success).
 // fold_q != 0: the residues of A plane l are (q_l r) mod p_l (symmetric) instead of r, with q_l the
 // CRT inverse of modulus l for the problem's N; the abs plane and B are unchanged.
-int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t s, int fold_q = 0);
+// fold_q: A residues carry the CRT inverses (production); packed: residue planes in the packed layout
+int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t s, int fold_q = 0, int packed = 0);
 // yd == nullptr: read the int32 planes of oz2_problem::C32 (kernel-level API); else the digits.
 // blocked: the digits and L of every problem are in the blocked layout (production, yd != nullptr)
 int recon_launch(const oz2_problem* d, const YDesc* yd, int num, int max_m, int max_n, hipStream_t s, int mode,
@@ -172,5 +184,6 @@ struct ggemm_handle_s {
   int* reuse_nmod;
   size_t *ua_off8, *ua_offs, *ub_off8, *ub_offs;
   int reuse_promote;   // GGEMM_REUSE_PROMOTE=1 at create: PROMOTE policy, else EXACT_N
-  int digits_colmajor; // GGEMM_DIGITS_COLMAJOR=1 at create: never the blocked digit layout (testing)
+  int digits_colmajor; // GGEMM_DIGITS_COLMAJOR=1 at create: row-major residues and column-major digits
+                       // only, the kernel-level layouts (testing)
 };

@@ -27,6 +27,8 @@
 // drains the prefetch ring.  The ring's own waits are explicit (s_waitcnt vmcnt(n) + s_barrier).
 // Bounds: rows >= m / n load (clamped) row m-1 / n-1 and only feed outputs that are not stored;
 // with kp % 64 == 32 the last stage's A chunks k >= kp are overwritten with zeros before use.
+// Operands: row-major residues (the kernel-level API) or, in the production pipeline, the packed
+// layout, where a stage's 64 k-bytes of 16 consecutive rows are one contiguous kilobyte.
 // Epilogue, per problem: int32 C (the reference contract, used by the kernel-level API and the
 // abs plane), or -- in the production pipeline -- one residue byte C mod p per entry (I8Epi),
 // which with q-folded A residues is the CRT digit; this cuts the plane write from 4 to 1 byte.
@@ -100,24 +102,56 @@ __device__ __forceinline__ void wait_barrier() {
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(VM) : "memory");
 }
 
+// Wait for this wave's LDS reads with every fragment register an operand of the wait, so that no
+// compiler-generated copy of a fragment can be placed before its data has arrived.
+template <int FM, int FN>
+__device__ __forceinline__ void lds_wait_frags(v4i (&a)[FM], v4i (&b)[FN]) {
+  if constexpr (FM == 8 && FN == 4) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]), "+v"(a[6]), "+v"(a[7]),
+                   "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]));
+  } else if constexpr (FM == 4 && FN == 4) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]));
+  } else {
+    static_assert(FM == 2 && FN == 2, "fragment counts");
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a[0]), "+v"(a[1]), "+v"(b[0]), "+v"(b[1]));
+  }
+}
+
+// One k-stage of an operand: the address of its tile's first row, the byte stride between rows and
+// the valid bytes per row (chunks at or past it load chunk 0 instead; A's are zeroed in LDS).
+struct StageSrc {
+  const int8_t* base;
+  int stride, lim;
+};
+// row-major residues (rows x kp, the kernel-level API) or the packed layout (production)
+__device__ __forceinline__ StageSrc stage_src(const int8_t* plane, int rows, int row0, int kp, int k0, bool packed) {
+  if (packed) {
+    const int b = k0 >> 6, rb = b == (kp >> 6) ? 32 : 64;
+    return StageSrc{plane + (size_t)b * rows * 64 + (size_t)row0 * rb, rb, rb};
+  }
+  return StageSrc{plane + (size_t)row0 * kp + k0, kp, kp - k0};
+}
+
 template <class C>
-__device__ __forceinline__ void dma_stage(const int8_t* A, const int8_t* B, int kp, int m_rem, int n_rem, int k0,
-                                          uint8_t* st, int wave, int lane) {
+__device__ __forceinline__ void dma_stage(const StageSrc& a, const StageSrc& b, int m_rem, int n_rem, uint8_t* st,
+                                          int wave, int lane) {
   const int r_in = lane >> 2, pc = lane & 3;
 #pragma unroll
   for (int q = 0; q < C::DA; ++q) {
     const int piece = wave + C::NW * q, row = piece * 16 + r_in;
-    const int kk = k0 + 16 * swz(row, pc);
+    const int kk = 16 * swz(row, pc);
     const int rr = row < m_rem ? row : m_rem - 1;
-    __builtin_amdgcn_global_load_lds((const void*)(A + (size_t)rr * kp + (kk < kp ? kk : 0)),
+    __builtin_amdgcn_global_load_lds((const void*)(a.base + (size_t)rr * a.stride + (kk < a.lim ? kk : 0)),
                                      GGEMM_LDS(st + piece * 1024), 16, 0, 0);
   }
 #pragma unroll
   for (int q = 0; q < C::DB; ++q) {
     const int piece = wave + C::NW * q, row = piece * 16 + r_in;
-    const int kk = k0 + 16 * swz(row, pc);
+    const int kk = 16 * swz(row, pc);
     const int rr = row < n_rem ? row : n_rem - 1;
-    __builtin_amdgcn_global_load_lds((const void*)(B + (size_t)rr * kp + (kk < kp ? kk : 0)),
+    __builtin_amdgcn_global_load_lds((const void*)(b.base + (size_t)rr * b.stride + (kk < b.lim ? kk : 0)),
                                      GGEMM_LDS(st + C::SA + piece * 1024), 16, 0, 0);
   }
 }
@@ -131,7 +165,7 @@ __device__ __forceinline__ uint32_t residue_byte(int32_t c, const I8Epi& e) {
   return (uint32_t)(r + (r < 0 ? (int)e.p : 0));
 }
 
-template <class C>
+template <class C, bool kPacked>
 __device__ __forceinline__ void run_tile(uint8_t* lds, const i8_problem& P, const I8Epi& epi, int tm, int tn) {
   constexpr int FM = C::FM, FN = C::FN, NST = C::NST;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -139,9 +173,11 @@ __device__ __forceinline__ void run_tile(uint8_t* lds, const i8_problem& P, cons
   const int row0 = tm * C::BM, col0 = tn * C::BN;
   const int m_rem = P.m - row0, n_rem = P.n - col0;
   const int kp = P.kp;
-  const int8_t* A = P.A + (size_t)row0 * kp;
-  const int8_t* B = P.B + (size_t)col0 * kp;
   const int nk = (kp + kBK - 1) / kBK;
+  auto load = [&](int kt, uint8_t* st) {
+    dma_stage<C>(stage_src(P.A, P.m, row0, kp, kt * kBK, kPacked), stage_src(P.B, P.n, col0, kp, kt * kBK, kPacked),
+                 m_rem, n_rem, st, wave, lane);
+  };
 
   // fragment addresses: rows wm WM + 16 i + lane % 16 (A), wn WN + 16 j + lane % 16 (B), chunk lane / 16;
   // the swizzle depends on row / 2 mod 4 only, so blocks i, j sit at fixed 1 KB immediates
@@ -159,7 +195,7 @@ __device__ __forceinline__ void run_tile(uint8_t* lds, const i8_problem& P, cons
 
 #pragma unroll
   for (int q = 0; q < NST - 1; ++q)
-    if (q < nk) dma_stage<C>(A, B, kp, m_rem, n_rem, q * kBK, lds + q * C::STAGE, wave, lane);
+    if (q < nk) load(q, lds + q * C::STAGE);
   int buf = 0;
   for (int kt = 0; kt < nk; ++kt) {
     // stage kt landed (the NST - 2 stages after it may still be in flight; near the end fewer
@@ -168,7 +204,7 @@ __device__ __forceinline__ void run_tile(uint8_t* lds, const i8_problem& P, cons
     if (kt + NST - 1 < nk) {
       int b2 = buf + NST - 1;   // the ring slot of stage kt - 1
       if (b2 >= NST) b2 -= NST;
-      dma_stage<C>(A, B, kp, m_rem, n_rem, (kt + NST - 1) * kBK, lds + b2 * C::STAGE, wave, lane);
+      load(kt + NST - 1, lds + b2 * C::STAGE);
     }
     uint8_t* st = lds + buf * C::STAGE;
     if (kt == nk - 1 && (kp & 63)) {   // k in [kp, kp + 32): zero A's chunks 2, 3
@@ -182,12 +218,7 @@ __device__ __forceinline__ void run_tile(uint8_t* lds, const i8_problem& P, cons
     v4i a[FM], b[FN];
     read_frags<FN, C::SA>(b, b_addr + so);
     read_frags<FM, 0>(a, a_addr + so);
-    // the fragments are valid after this wait: every fragment is an operand of it
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a[0]), "+v"(b[0]), "+v"(a[FM - 1]), "+v"(b[FN - 1]));
-#pragma unroll
-    for (int i = 1; i < FM - 1; ++i) asm volatile("" : "+v"(a[i]));
-#pragma unroll
-    for (int j = 1; j < FN - 1; ++j) asm volatile("" : "+v"(b[j]));
+    lds_wait_frags<FM, FN>(a, b);   // the fragments are valid after this wait
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -310,9 +341,9 @@ __global__ void __launch_bounds__(kThreads, 2) i8_grouped_kernel(const i8_proble
   int tm, tn;
   raster(t.local, P.m, P.n, i8_tile_m(t.cfg), i8_tile_n(t.cfg), tm, tn);
   switch (t.cfg) {
-    case 0: run_tile<Cfg0>(lds, P, epi, tm, tn); break;
-    case 1: run_tile<Cfg1>(lds, P, epi, tm, tn); break;
-    default: run_tile<Cfg2>(lds, P, epi, tm, tn); break;
+    case 0: (epi.mode & kEpiPacked) ? run_tile<Cfg0, true>(lds, P, epi, tm, tn) : run_tile<Cfg0, false>(lds, P, epi, tm, tn); break;
+    case 1: (epi.mode & kEpiPacked) ? run_tile<Cfg1, true>(lds, P, epi, tm, tn) : run_tile<Cfg1, false>(lds, P, epi, tm, tn); break;
+    default: (epi.mode & kEpiPacked) ? run_tile<Cfg2, true>(lds, P, epi, tm, tn) : run_tile<Cfg2, false>(lds, P, epi, tm, tn); break;
   }
 }
 
@@ -327,7 +358,8 @@ __global__ void __launch_bounds__(kThreadsL, 1) i8_large_kernel(const i8_problem
   if (epis) epi = epis[t.pi];
   int tm, tn;
   raster(t.local, P.m, P.n, CfgL::BM, CfgL::BN, tm, tn);
-  run_tile<CfgL>(lds, P, epi, tm, tn);
+  if (epi.mode & kEpiPacked) run_tile<CfgL, true>(lds, P, epi, tm, tn);
+  else run_tile<CfgL, false>(lds, P, epi, tm, tn);
 }
 
 // ----------------------------------------------------------------------------- host side

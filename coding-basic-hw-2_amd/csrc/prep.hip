@@ -181,7 +181,7 @@ struct PrepShared {
 
 // ------------------------------------------------------------------------------- A rows
 __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ tab, int blk, int split,
-                          int nsplit, PrepShared& sm, unsigned long long* cnt, int widx) {
+                          int nsplit, PrepShared& sm, unsigned long long* cnt, int widx, bool packed) {
   const int tid = threadIdx.x;
   const int N = pr.num_moduli, K = pr.k, Kp = pr.kp, m = pr.m;
   const int row0 = blk * kARows;
@@ -284,7 +284,7 @@ __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ t
     __syncthreads();
     const int kb = k0 + 16 * seg;
     if (t >= w0 && t < w1 && rvalid && kb < Kp) {
-      int8_t* dst = pr.A8 + (size_t)(row0 + rr) * Kp + kb;
+      int8_t* dst = pr.A8 + (packed ? packed_offset(row0 + rr, kb, m, Kp) : (size_t)(row0 + rr) * Kp + kb);
       if (nf_r) {
         for (int l = 0; l <= N; ++l)
           *reinterpret_cast<uint4*>(dst + (size_t)l * pr.a8_mod_stride) = make_uint4(0u, 0u, 0u, 0u);
@@ -329,7 +329,7 @@ __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ t
 
 // ---------------------------------------------------------------------------- B columns
 __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ tab, int blk, int split,
-                          int nsplit, PrepShared& sm, unsigned long long* cnt) {
+                          int nsplit, PrepShared& sm, unsigned long long* cnt, bool packed) {
   const int lane = threadIdx.x & 31, w = threadIdx.x >> 5;
   const int j = blk * kBCols + w;
   const int n = pr.n, N = pr.num_moduli, K = pr.k, Kp = pr.kp;
@@ -377,7 +377,7 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
   const bool nf = sh == OZ2_SHIFT_NONFINITE;
 
   double da2 = 0.0, na2 = 0.0;
-  int8_t* base = pr.B8 + (size_t)j * Kp;
+  int8_t* const B8 = pr.B8;
   const int nchunk = (Kp + 127) / 128;
   const int per = (nchunk + nsplit - 1) / nsplit;
   const int c0 = min(nchunk, split * per), c1 = min(nchunk, c0 + per);
@@ -386,13 +386,14 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
   for (int ch = (split == 0 ? 0 : c0); ch < (split == 0 ? nchunk : c1); ++ch) {
     const int k0 = 128 * ch + 4 * lane;
     if (k0 >= Kp) continue;
+    int8_t* const base = B8 + (packed ? packed_offset(j, k0, n, Kp) : (size_t)j * Kp + k0);
     double a[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) a[e] = (k0 + e < K) ? b[k0 + e] : 0.0;
     const bool write = ch >= c0 && ch < c1;
     if (nf) {
       if (write)
-        for (int l = 0; l <= N; ++l) *reinterpret_cast<uint32_t*>(base + (size_t)l * pr.b8_mod_stride + k0) = 0u;
+        for (int l = 0; l <= N; ++l) *reinterpret_cast<uint32_t*>(base + (size_t)l * pr.b8_mod_stride) = 0u;
       continue;
     }
     int q0[4], q1[4], q2[4], E[4];
@@ -414,12 +415,12 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
     for (int l = 0; l < N; ++l) {
       uint32_t q;
       residue_bytes<4>(q0, q1, q2, E, wE, plane_c(tab, l, 0), sm.pow2[l], &q);
-      *reinterpret_cast<uint32_t*>(base + (size_t)l * pr.b8_mod_stride + k0) = q;
+      *reinterpret_cast<uint32_t*>(base + (size_t)l * pr.b8_mod_stride) = q;
     }
     uint32_t q = 0u;
 #pragma unroll
     for (int e = 0; e < 4; ++e) q |= abs_u8(a[e], sg) << (8 * e);
-    *reinterpret_cast<uint32_t*>(base + (size_t)N * pr.b8_mod_stride + k0) = q;
+    *reinterpret_cast<uint32_t*>(base + (size_t)N * pr.b8_mod_stride) = q;
   }
   if (split != 0) return;
 #pragma unroll
@@ -435,7 +436,8 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
 
 __global__ void __launch_bounds__(kThreads) prep_kernel(const oz2_problem* __restrict__ probs, int a_blocks,
                                                         const CrtTables* __restrict__ tab,
-                                                        unsigned long long* __restrict__ cnt, int fold_q) {
+                                                        unsigned long long* __restrict__ cnt, int fold_q,
+                                                        int packed) {
   __shared__ PrepShared sm;
   const oz2_problem& pr = probs[blockIdx.y];
   const int N = pr.num_moduli;
@@ -452,9 +454,9 @@ __global__ void __launch_bounds__(kThreads) prep_kernel(const oz2_problem* __res
   const int blk = (int)blockIdx.x;
   if (blk < a_blocks) {
     if (blk * kARows >= pr.m) return;
-    prep_rows(pr, tab, blk, blockIdx.z, gridDim.z, sm, cnt, fold ? N : 0);
+    prep_rows(pr, tab, blk, blockIdx.z, gridDim.z, sm, cnt, fold ? N : 0, packed != 0);
   } else {
-    prep_cols(pr, tab, blk - a_blocks, blockIdx.z, gridDim.z, sm, cnt);
+    prep_cols(pr, tab, blk - a_blocks, blockIdx.z, gridDim.z, sm, cnt, packed != 0);
   }
 }
 
@@ -462,7 +464,7 @@ int g_force_split = 0;
 
 }  // namespace
 
-int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t s, int fold_q) {
+int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t s, int fold_q, int packed) {
   if (num <= 0) return 0;
   if (num > 65535 || max_m < 0 || max_n < 0) return 1;
   DevCtx* c = dev_ctx();
@@ -475,7 +477,7 @@ int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t
   int S = (int)std::min<long long>(16, std::max<long long>(1, (target + blocks - 1) / blocks));
   if (g_force_split > 0) S = g_force_split;
   hipLaunchKernelGGL(prep_kernel, dim3(a_blocks + b_blocks, num, S), dim3(kThreads), 0, s, d, a_blocks,
-                     c->tab, c->counters, fold_q);
+                     c->tab, c->counters, fold_q, packed);
   return hipGetLastError() == hipSuccess ? 0 : 3;
 }
 

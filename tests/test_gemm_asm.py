@@ -1,0 +1,36 @@
+"""The INT8 GEMM's fragment reads are inline-assembly LDS loads whose waits the compiler cannot
+see.  Compile csrc/i8gemm.hip for gfx950 and check, by dataflow over each kernel's assembly, that
+no instruction uses a fragment register before the s_waitcnt that covers its load (CPU only).
+The checker itself is tested on a hand-written fragment with one such use."""
+import subprocess
+from pathlib import Path
+
+import pytest
+
+import lds_wait_check as L
+
+REPO = Path(__file__).resolve().parents[1]
+CSRC = REPO / "coding-basic-hw-2_amd" / "csrc"
+
+
+def test_checker_finds_a_stale_read():
+    asm = ["k:", "\tds_read_b128 v[10:13], v1 offset:16", "\ts_cbranch_scc1 .LBB0_2", "\tv_mov_b32 v20, v11",
+           ".LBB0_2:", "\ts_waitcnt lgkmcnt(0)", "\tv_mov_b32 v21, v12", "\ts_endpgm"]
+    found = L.check_lines(asm, "k")
+    assert [(b, t) for b, t, _ in found] == [("__entry", "v_mov_b32 v20, v11")]
+    asm2 = ["k:", "\tds_read_b128 v[10:13], v1", "\tds_read_b128 v[14:17], v1 offset:64", "\ts_waitcnt lgkmcnt(1)",
+            "\tv_mov_b32 v20, v11", "\tv_mov_b32 v21, v15", "\ts_endpgm"]
+    assert [t for _, t, _ in L.check_lines(asm2, "k")] == ["v_mov_b32 v21, v15"]
+
+
+def test_int8_gemm_kernels_wait_before_use(tmp_path):
+    out = tmp_path / "i8gemm.s"
+    cmd = ["/opt/rocm/bin/hipcc", "-O3", "-std=c++17", "-fPIC", f"-I{REPO / 'include'}", f"-I{CSRC}", "-x", "hip",
+           "--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+           "-Wno-unused-command-line-argument", "--cuda-device-only", "-S", str(CSRC / "i8gemm.hip"), "-o", str(out)]
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+    if r.returncode != 0:
+        pytest.fail(r.stderr[-2000:])
+    for kernel in ("i8_grouped_kernel", "i8_large_kernel"):
+        found = L.check(out, kernel)
+        assert not found, f"{kernel}: {found[:4]}"

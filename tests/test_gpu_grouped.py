@@ -202,10 +202,10 @@ def test_large_tile_kernel_mixed_k_stream():
                                     [(520, 600, 470)] * 3],                                   # large-tile kernel
                          ids=["general", "large"])
 def test_blocked_and_columnmajor_digits_same_bits(shapes):
-    """The CRT digits and abs-plane products travel from the INT8 GEMM to the reconstruct in the
-    blocked 16 x 16 layout when the padded planes fit the workspace, else column-major
-    (GGEMM_DIGITS_COLMAJOR=1 forces it).  Both give the oracle's bits; m, n are not multiples of
-    16, so the blocked planes carry padding."""
+    """The production layouts -- residue planes packed in 64-byte k-blocks, CRT digits and
+    abs-plane products in 16 x 16 blocks -- against the kernel-level ones (row-major residues,
+    column-major digits; GGEMM_DIGITS_COLMAJOR=1 forces them).  Both give the oracle's bits; m, n
+    are not multiples of 16 (padded blocks) and kp = 96, 224, 480 end in a 32-byte half block."""
     case = Case(shapes, 20261208, phi=0.5, beta=0.5)
     say("blocked vs column-major digits")
     outs = []
