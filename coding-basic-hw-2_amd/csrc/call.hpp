@@ -21,6 +21,7 @@ struct GroupedCall {
   int ne = 0, nn = 0;             // emulated / native problems
   size_t n_i8 = 0;                // (problem, plane) INT8 products
   int max_m = 0, max_n = 0;
+  int nmax = 0;                   // largest num_moduli among the emulated problems
   int nprep = 0;                  // operand reuse: prep descriptors (0: prep runs on the ne problems)
   int pmax_m = 0, pmax_n = 0;     // prep grid over the unique operands
   BlobLayout L{};

@@ -13,7 +13,6 @@ namespace ggemm {
 
 constexpr int kMaxModuli = GGEMM_MAX_MODULI;
 constexpr int kMaxPlanes = kMaxModuli + OZ2_EXTRA_PLANES;   // residues + abs plane
-constexpr int kPow2Table = 128;                             // 2^e mod p tabulated for e < 128
 constexpr int kS2Bits = 18;                                 // fractional bits of s2
 constexpr int kKpAlign = 32;                                // Kp = round_up(k, 32)
 constexpr size_t kBufAlign = 256;                           // byte alignment of every block
@@ -26,11 +25,16 @@ inline int kp_of(int k) { return (int)align_up((size_t)k, kKpAlign); }
 struct CrtTables {
   int32_t p[kMaxModuli];
   uint32_t magic[kMaxModuli];                  // floor(2^32 / p)
-  double inv_p_up[kMaxModuli];                 // 1 / p rounded up to a double
-  int32_t Kp[kMaxModuli];                      // p ceil(2^28 / p)
-  double h_ip_up[kMaxModuli];                  // floor(p / 2) inv_p_up, rounded up
-  int32_t w3[kMaxModuli + 1][kMaxModuli][3];   // [0][l]: 2^(18 i) mod p_l; [N][l]: q_(N,l) 2^(18 i) mod p_l
-  uint8_t pow2[kMaxModuli][kPow2Table];        // 2^e mod p
+  float ipf[kMaxModuli];                       // 1 / p, nearest float
+  float cf[kMaxModuli];                        // (floor(p / 2) + 1/2) / p + 2048, nearest float
+  // byte weights of the digit words, four per word, for word kind k:
+  //   k = 0: unsigned bytes 2^(8 i) mod p, i = 0..3        (low word, unsigned digits)
+  //   k = 1: unsigned bytes 2^(8 i) mod p, i = 4..7        (wide middle word, unsigned digits)
+  //   k = 2: signed bytes sym(2^(8 i) mod p), i = 4..7     (narrow top word, signed digits)
+  //   k = 3: signed bytes sym(2^(8 i) mod p), i = 8..11    (wide top word, signed digits)
+  // [0][l][k] plain, [N][l][k] with the CRT inverse q_(N,l) folded in (q 2^(8 i) mod p);
+  // sym(r) in [-floor(p/2), p - 1 - floor(p/2)]
+  uint32_t wb[kMaxModuli + 1][kMaxModuli][4];
   uint64_t s1[kMaxModuli + 1][kMaxModuli];     // floor(M_l / u1)
   uint32_t s2[kMaxModuli + 1][kMaxModuli];     // round(frac(M_l / u1) 2^18)
   int32_t qinv[kMaxModuli + 1][kMaxModuli];    // M_l^-1 mod p_l
@@ -143,7 +147,9 @@ int f64_launch(const F64Problem* d_probs, const void* d_sched, int total_tiles, 
 // fold_q != 0: the residues of A plane l are (q_l r) mod p_l (symmetric) instead of r, with q_l the
 // CRT inverse of modulus l for the problem's N; the abs plane and B are unchanged.
 // fold_q: A residues carry the CRT inverses (production); packed: residue planes in the packed layout
-int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t s, int fold_q = 0, int packed = 0);
+// max_moduli: the largest num_moduli among the num problems (selects the digit width)
+int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t s, int fold_q, int packed,
+                int max_moduli);
 // yd == nullptr: read the int32 planes of oz2_problem::C32 (kernel-level API); else the digits.
 // blocked: the digits and L of every problem are in the blocked layout (production, yd != nullptr)
 int recon_launch(const oz2_problem* d, const YDesc* yd, int num, int max_m, int max_n, hipStream_t s, int mode,

@@ -76,6 +76,25 @@ double to_double(const U192& a) {
   return (double)v;
 }
 
+// r in [0, p) as the byte of its symmetric representative in [-floor(p/2), p - 1 - floor(p/2)]
+uint32_t sym_byte(uint32_t r, uint32_t p) {
+  const int v = (int)r > (int)(p - 1 - p / 2) ? (int)r - (int)p : (int)r;
+  return (uint32_t)v & 0xffu;
+}
+
+// the four weight words of CrtTables::wb for modulus p and multiplier q
+void digit_weights(uint32_t p, uint32_t q, uint32_t* w) {
+  uint32_t e[12];   // q 2^(8 i) mod p
+  e[0] = q % p;
+  for (int i = 1; i < 12; ++i) e[i] = (e[i - 1] * 256u) % p;
+  for (int b = 0; b < 4; ++b) {
+    w[0] |= e[b] << (8 * b);
+    w[1] |= e[4 + b] << (8 * b);
+    w[2] |= sym_byte(e[4 + b], p) << (8 * b);
+    w[3] |= sym_byte(e[8 + b], p) << (8 * b);
+  }
+}
+
 int build(CrtTables* t) {
   std::memset(t, 0, sizeof *t);
   for (int a = 0; a < kMaxModuli; ++a)
@@ -88,16 +107,9 @@ int build(CrtTables* t) {
     const uint32_t p = (uint32_t)kModuli[l];
     t->p[l] = (int32_t)p;
     t->magic[l] = (uint32_t)((1ull << 32) / p);
-    double ip = 1.0 / (double)p;
-    if (std::fma(ip, (double)p, -1.0) < 0.0) ip = std::nextafter(ip, 1.0);   // fma is exact here
-    t->inv_p_up[l] = ip;
-    t->Kp[l] = (int32_t)(p * (((1u << 28) + p - 1) / p));
-    double hip = (double)(p / 2) * ip;
-    if (std::fma((double)(p / 2), ip, -hip) > 0.0) hip = std::nextafter(hip, 1.0);
-    t->h_ip_up[l] = hip;
-    uint32_t v = 1 % p;
-    for (int e = 0; e < kPow2Table; ++e) { t->pow2[l][e] = (uint8_t)v; v = (2 * v) % p; }
-    for (int i = 0; i < 3; ++i) t->w3[0][l][i] = t->pow2[l][18 * i];
+    t->ipf[l] = (float)(1.0 / (double)p);
+    t->cf[l] = (float)(((double)(p / 2) + 0.5) / (double)p + 2048.0);
+    digit_weights(p, 1u, t->wb[0][l]);
   }
   for (int N = 1; N <= kMaxModuli; ++N) {
     U192 P;
@@ -114,8 +126,7 @@ int build(CrtTables* t) {
         if ((mr * x) % p == 1 % p) { inv = (int)x; break; }
       if (inv < 0) return 4;
       t->qinv[N][l] = inv;
-      for (int i = 0; i < 3; ++i)
-        t->w3[N][l][i] = (int32_t)(((uint32_t)t->pow2[l][18 * i] * (uint32_t)inv) % (uint32_t)kModuli[l]);
+      digit_weights(p, (uint32_t)inv, t->wb[N][l]);
       top = std::max(top, bit_length(M[l]));
     }
     const int sh = top - 49;   // u1 = 2^sh keeps every M_l / u1 below 2^49

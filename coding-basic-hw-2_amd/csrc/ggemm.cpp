@@ -189,6 +189,7 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
     st->num_fallback += (r != GGEMM_ROUTE_EMU && r != GGEMM_ROUTE_EMPTY && r != GGEMM_ROUTE_K_ZERO &&
                          r != GGEMM_ROUTE_ALPHA_ZERO);
   }
+  c.nmax = nmax;
   st->moduli_min = c.ne ? GGEMM_MAX_MODULI : 0;
   st->moduli_max = nmax;
   for (int j = 0; j < c.ne; ++j) st->moduli_min = std::min(st->moduli_min, plan[emu_idx[j]].num_moduli);
@@ -322,7 +323,7 @@ int enqueue_grouped(const GroupedCall& c, const char* db, hipStream_t s, int rep
   if (c.ne > 0) {
     const bool shared = c.nprep > 0;   // operand reuse: prep once per unique operand
     if (prep_launch(shared ? reinterpret_cast<const oz2_problem*>(db + c.L.off_prep) : doz, shared ? c.nprep : c.ne,
-                    shared ? c.pmax_m : c.max_m, shared ? c.pmax_n : c.max_n, s, 1, c.packed))
+                    shared ? c.pmax_m : c.max_m, shared ? c.pmax_n : c.max_n, s, 1, c.packed, c.nmax))
       return GGEMM_ERR_NUMERICS;
     ++*launches;
     prof::mark(prof_set, 1, s);
@@ -461,7 +462,10 @@ int path_emu_loop(ggemm_handle_t h, bool batched, const ggemm_problem_t* probs, 
   q = 0;
   for (int j = 0; j < c.ne && !r; ++j) {
     const int planes = hoz[j].num_moduli + OZ2_EXTRA_PLANES;
-    if (prep_launch(doz + j, 1, hoz[j].m, hoz[j].n, h->stream, 1, c.packed)) { r = GGEMM_ERR_NUMERICS; break; }
+    if (prep_launch(doz + j, 1, hoz[j].m, hoz[j].n, h->stream, 1, c.packed, hoz[j].num_moduli)) {
+      r = GGEMM_ERR_NUMERICS;
+      break;
+    }
     ++nl;
     if (batched) {
       if (i8_launch(di8 + q, depi + q, db + base + j * per, &h->loop_info[j], h->stream)) { r = GGEMM_ERR_I8GEMM; break; }

@@ -85,85 +85,120 @@ __device__ __forceinline__ int32_t norm_ub_bits(double x) {
   return b;
 }
 
-// Residues of an integer-valued double x (|x| < 2^81): x = sign M 2^E with M < 2^53 split in
-// 18-bit chunks; x mod p = sign (c0 [2^E] + c1 [2^(E+18)] + c2 [2^(E+36)]) mod p.
-struct Split {
-  uint32_t c0, c1, c2;
-  int E;
-  bool neg;
+// Residues from the bytes of an integer-valued double x, |x| <= T_N < 2^77 (every row / column is
+// scaled into the norm budget T_N).  Exact floor splits at 2^32 write x in 32-bit words,
+//   narrow (T_N < 1.5 2^62, N <= 16): x = L + H 2^32,            L in [0, 2^32), |H| < 2^31
+//   wide:                             x = L + M 2^32 + H 2^64,   L, M in [0, 2^32), |H| < 2^13
+// L and M are used as unsigned bytes, H as balanced signed digits: the bytes of H + 0x80808080
+// minus 128 (H + 0x80808080 lies in [0, 2^32), so nothing wraps).  For a modulus p, with byte
+// weights 2^(8 i) mod p for the unsigned words and sym(2^(8 i) mod p) for H (times q for folded
+// planes):
+//   u = v_dot4_u32_u8 over L (and M), then v_dot4_i32_i8 over H; u = x (mod p) and
+//       -2^16 <= u < 2^19 + 2^16 (unsigned words give [0, 8 255^2], the signed one [-2^16, 2^16])
+//   q = trunc(fmaf(u, ipf, cf)) = floor((u + h) / p) + 2048, h = floor(p / 2), where ipf and
+//       cf = (h + 1/2)/p + 2048 are the nearest floats: the exact value (u + h + 1/2)/p + 2048 is
+//       positive and below 2^13, its fractional part (j + 1/2)/p is at least 1/(2p) >= 2^-9 from an
+//       integer, and the computed one is within |u| 2^-32 + 2^-13 + 2^-12 < 2^-10 of it (checked
+//       exhaustively over every u and p on the host)
+//   r = u - q p = sym(x mod p) - 2048 p, and 2048 p = 0 (mod 256): its low byte is the stored
+//       byte of the symmetric residue in [-h, p - 1 - h]
+// Full-rate 32-bit operations only: two or three dot products, three float operations and one
+// 24-bit multiply-add per residue, no table lookups.  The bytes equal the reference's
+// reduce / negate / symmetric-map sequence (sym(x mod p) is unique).
+template <bool kWide>
+struct Digits {
+  uint32_t w[kWide ? 3 : 2];   // L, (M,) balanced H
 };
-__device__ __forceinline__ Split split_int(double x) {
-  Split d;
-  const double ax = fabs(x);
-  d.neg = x < 0.0;
-  uint64_t M;
-  int E;
-  if (ax < 9007199254740992.0) {
-    M = (uint64_t)ax;
-    E = 0;
-  } else {
-    const uint64_t b = (uint64_t)__double_as_longlong(ax);
-    E = min((int)((b >> 52) & 0x7ff) - 1075, kPow2Table - 37);
-    M = (b & ((1ull << 52) - 1)) | (1ull << 52);
+template <bool kWide>
+__device__ __forceinline__ Digits<kWide> digits_of(double x) {
+  Digits<kWide> d;
+  double h = floor(x * 0x1p-32);   // x = h 2^32 + L: exact
+  d.w[0] = (uint32_t)fma(-h, 0x1p32, x);
+  if (kWide) {
+    const double t = floor(h * 0x1p-32);
+    d.w[1] = (uint32_t)fma(-t, 0x1p32, h);
+    h = t;
   }
-  d.c0 = (uint32_t)(M & 0x3ffff);
-  d.c1 = (uint32_t)((M >> 18) & 0x3ffff);
-  d.c2 = (uint32_t)(M >> 36);
-  d.E = E;
+  d.w[kWide ? 2 : 1] = ((uint32_t)(int)h + 0x80808080u) ^ 0x80808080u;
   return d;
 }
-// Symmetric residues sym(x mod p) in [-h, p - 1 - h] (h = floor(p / 2)) of integers
-// x = c0 2^E + c1 2^(E+18) + c2 2^(E+36) given as signed 18-bit chunks (the sign of x on each):
-//   u = c0 w0 + c1 w1 + c2 w2 + K p,  w_i = 2^(E + 18 i) mod p (times q for folded planes)
-//       (24-bit multiply-adds; |c_i w_i| < 2^26, K p >= 2^28, so 0 < u < 2^30)
-//   q = trunc(fma(u, ip, hip)) = floor((u + h) / p)
-//       exact: ip = 1/p and hip = h ip are rounded up, so the fma's exact value is >= (u + h)/p,
-//       and it exceeds it by less than 2^-21 / p while (u + h)/p <= floor + 1 - 1/p
-//   r = fma(-q, p, u)                 (exact: an integer in [-h, p - 1 - h])
-// The byte equals the reference's reduce / negate / symmetric-map sequence; every operation is
-// full rate (24-bit integer and FP64 arithmetic, no 32-bit integer multiply).  When no lane of the
-// wave has E > 0 the weights are per-plane constants (scalar registers), otherwise per-element
-// LDS table lookups.
-struct PlaneC {
-  int Kp, w0, w1, w2;
-  double p, ip, hip;
+struct PlaneW {
+  uint32_t w0, w1;
+  int wh, p;
+  float ip, c;
 };
-__device__ __forceinline__ PlaneC plane_c(const CrtTables* __restrict__ tab, int l, int widx) {
-  return PlaneC{tab->Kp[l], tab->w3[widx][l][0], tab->w3[widx][l][1], tab->w3[widx][l][2],
-                (double)tab->p[l], tab->inv_p_up[l], tab->h_ip_up[l]};
+template <bool kWide>
+__device__ __forceinline__ PlaneW plane_w(const CrtTables* __restrict__ tab, int l, int widx) {
+  const uint32_t* w = tab->wb[widx][l];
+  return PlaneW{w[0], w[1], (int)w[kWide ? 3 : 2], tab->p[l], tab->ipf[l], tab->cf[l]};
 }
-template <int NE>
-__device__ __forceinline__ void residue_bytes(const int* c0, const int* c1, const int* c2, const int* E, bool anyE,
-                                              const PlaneC& k, const uint8_t* pw, uint32_t* out) {
-  int u[NE];
-  if (!anyE) {
+__device__ __forceinline__ uint32_t pack4(int r0, int r1, int r2, int r3) {   // low bytes
+  const uint32_t lo = __builtin_amdgcn_perm((uint32_t)r1, (uint32_t)r0, 0x0c0c0400u);
+  const uint32_t hi = __builtin_amdgcn_perm((uint32_t)r3, (uint32_t)r2, 0x0c0c0400u);
+  return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+}
+template <int NE, bool kWide>
+__device__ __forceinline__ void residue_bytes(const Digits<kWide>* x, const PlaneW& k, uint32_t* out) {
+  // groups of up to 8 values, phase by phase, so that dependent dot products are not back to
+  // back and few temporaries are live
+  constexpr int G = NE < 8 ? NE : 8;
 #pragma unroll
-    for (int e = 0; e < NE; ++e) u[e] = __mul24(c0[e], k.w0) + __mul24(c1[e], k.w1) + __mul24(c2[e], k.w2) + k.Kp;
+  for (int g = 0; g < NE; g += G) {
+    uint32_t s[G];
+    int u[G], r[G];
+#pragma unroll
+    for (int e = 0; e < G; ++e) s[e] = __builtin_amdgcn_udot4(x[g + e].w[0], k.w0, 0u, false);
+    if (kWide) {
+#pragma unroll
+      for (int e = 0; e < G; ++e) s[e] = __builtin_amdgcn_udot4(x[g + e].w[1], k.w1, s[e], false);
+    }
+#pragma unroll
+    for (int e = 0; e < G; ++e) u[e] = __builtin_amdgcn_sdot4((int)x[g + e].w[kWide ? 2 : 1], k.wh, (int)s[e], false);
+#pragma unroll
+    for (int e = 0; e < G; ++e) r[e] = (int)__builtin_fmaf((float)u[e], k.ip, k.c);
+#pragma unroll
+    for (int e = 0; e < G; ++e) r[e] = __mul24(r[e], -k.p) + u[e];
+#pragma unroll
+    for (int w = 0; w < G / 4; ++w) out[g / 4 + w] = pack4(r[4 * w], r[4 * w + 1], r[4 * w + 2], r[4 * w + 3]);
+  }
+}
+// x 2^sh for NE values (mul_pow2 of each), the scale formed once when |sh| <= 1000 (the common case)
+template <int NE>
+__device__ __forceinline__ void scaled(const double* x, int sh, double* out) {
+  if (sh >= -1000 && sh <= 1000) {
+    const double sc = pow2d(sh);
+#pragma unroll
+    for (int e = 0; e < NE; ++e) out[e] = x[e] * sc;
   } else {
 #pragma unroll
-    for (int e = 0; e < NE; ++e)
-      u[e] = __mul24(c0[e], (int)pw[E[e]]) + __mul24(c1[e], (int)pw[E[e] + 18]) + __mul24(c2[e], (int)pw[E[e] + 36]) + k.Kp;
-  }
-#pragma unroll
-  for (int w = 0; w < NE / 4; ++w) {
-    uint32_t v = 0u;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const double ud = (double)u[4 * w + e];
-      const double q = trunc(fma(ud, k.ip, k.hip));
-      const int r = (int)fma(-q, k.p, ud);
-      v |= ((uint32_t)r & 0xffu) << (8 * e);
-    }
-    out[w] = v;
+    for (int e = 0; e < NE; ++e) out[e] = mul_pow2(x[e], sh);
   }
 }
-// signed chunks of an integer-valued double (|x| < 2^81)
-__device__ __forceinline__ void chunks(double x, int& c0, int& c1, int& c2, int& E) {
-  const Split d = split_int(x);
-  c0 = d.neg ? -(int)d.c0 : (int)d.c0;
-  c1 = d.neg ? -(int)d.c1 : (int)d.c1;
-  c2 = d.neg ? -(int)d.c2 : (int)d.c2;
-  E = d.E;
+// Residue planes 0..N-1 of NE consecutive k (integer-valued doubles) of one row / column: NE bytes
+// per plane at dst + l * stride (one 128-bit or 32-bit store).  Three-word digits of 16 values
+// take two passes of 8 (64-bit stores), which keeps the kernel's register count for the common
+// two-word case.
+template <int NE, bool kWide>
+__device__ __forceinline__ void planes(const double* xt, int N, const CrtTables* __restrict__ tab, int widx,
+                                       int8_t* dst, size_t stride) {
+  constexpr int P = (kWide && NE > 8) ? 8 : NE;   // values per pass
+#pragma unroll
+  for (int h = 0; h < NE; h += P) {
+    Digits<kWide> x[P];
+#pragma unroll
+    for (int e = 0; e < P; ++e) x[e] = digits_of<kWide>(xt[h + e]);
+    for (int l = 0; l < N; ++l) {
+      uint32_t q[P / 4];
+      residue_bytes<P, kWide>(x, plane_w<kWide>(tab, l, widx), q);
+      int8_t* d = dst + (size_t)l * stride + h;
+      if constexpr (P == 16)
+        *reinterpret_cast<uint4*>(d) = make_uint4(q[0], q[1], q[2], q[3]);
+      else if constexpr (P == 8)
+        *reinterpret_cast<uint2*>(d) = make_uint2(q[0], q[1]);
+      else
+        *reinterpret_cast<uint32_t*>(d) = q[0];
+    }
+  }
 }
 __device__ __forceinline__ uint32_t abs_u8(double a, int sig) {
   if (sig == OZ2_SHIFT_ZERO) return 0;
@@ -171,7 +206,6 @@ __device__ __forceinline__ uint32_t abs_u8(double a, int sig) {
 }
 
 struct PrepShared {
-  uint8_t pow2[kMaxModuli][kPow2Table];
   double red0[kChains][kARows];
   double red1[kChains][kARows];
   int shift[kARows], sig[kARows];
@@ -180,6 +214,7 @@ struct PrepShared {
 };
 
 // ------------------------------------------------------------------------------- A rows
+template <bool kWide>
 __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ tab, int blk, int split,
                           int nsplit, PrepShared& sm, unsigned long long* cnt, int widx, bool packed) {
   const int tid = threadIdx.x;
@@ -268,19 +303,19 @@ __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ t
       const int k = k0 + c + kChains * jj;
       av[jj] = (valid && k < K) ? A[i + (size_t)k * lda] : 0.0;
     }
+    if (!nf_c && split == 0) {
+      double xs[kATile / kChains];
+      scaled<kATile / kChains>(av, sh_c, xs);
 #pragma unroll
-    for (int jj = 0; jj < kATile / kChains; ++jj) {
-      const int kk = c + kChains * jj;
-      const double a = av[jj];
-      if (!nf_c && split == 0) {
-        const double xs = mul_pow2(a, sh_c);
-        const double xt = trunc(xs);
-        const double fr = xs - xt;
+      for (int jj = 0; jj < kATile / kChains; ++jj) {
+        const double xt = trunc(xs[jj]);
+        const double fr = xs[jj] - xt;
         da2 = fma(fr, fr, da2);
         na2 = fma(xt, xt, na2);
       }
-      sm.tile[kk][r] = a;
     }
+#pragma unroll
+    for (int jj = 0; jj < kATile / kChains; ++jj) sm.tile[c + kChains * jj][r] = av[jj];
     __syncthreads();
     const int kb = k0 + 16 * seg;
     if (t >= w0 && t < w1 && rvalid && kb < Kp) {
@@ -289,28 +324,21 @@ __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ t
         for (int l = 0; l <= N; ++l)
           *reinterpret_cast<uint4*>(dst + (size_t)l * pr.a8_mod_stride) = make_uint4(0u, 0u, 0u, 0u);
       } else {
-        int c0[16], c1[16], c2[16], E[16];
-        int anyE = 0;
+        double av[16], xt[16];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          chunks(trunc(mul_pow2(sm.tile[16 * seg + e][rr], sh_r)), c0[e], c1[e], c2[e], E[e]);
-          anyE |= E[e];
-        }
-        const bool wE = __any(anyE != 0);
-        for (int l = 0; l < N; ++l) {
-          const PlaneC pc = plane_c(tab, l, widx);
-          uint32_t q[4];
-          residue_bytes<16>(c0, c1, c2, E, wE, pc, sm.pow2[l], q);
-          *reinterpret_cast<uint4*>(dst + (size_t)l * pr.a8_mod_stride) = make_uint4(q[0], q[1], q[2], q[3]);
-        }
-        uint32_t q[4];
+        for (int e = 0; e < 16; ++e) av[e] = sm.tile[16 * seg + e][rr];
+        uint32_t q[4];   // abs plane first, so the A values are dead during the residue planes
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
           q[w] = 0u;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) q[w] |= abs_u8(sm.tile[16 * seg + 4 * w + e][rr], sg_r) << (8 * e);
+          for (int e = 0; e < 4; ++e) q[w] |= abs_u8(av[4 * w + e], sg_r) << (8 * e);
         }
         *reinterpret_cast<uint4*>(dst + (size_t)N * pr.a8_mod_stride) = make_uint4(q[0], q[1], q[2], q[3]);
+        scaled<16>(av, sh_r, xt);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) xt[e] = trunc(xt[e]);
+        planes<16, kWide>(xt, N, tab, widx, dst, pr.a8_mod_stride);
       }
     }
     __syncthreads();
@@ -328,6 +356,7 @@ __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ t
 }
 
 // ---------------------------------------------------------------------------- B columns
+template <bool kWide>
 __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ tab, int blk, int split,
                           int nsplit, PrepShared& sm, unsigned long long* cnt, bool packed) {
   const int lane = threadIdx.x & 31, w = threadIdx.x >> 5;
@@ -396,27 +425,19 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
         for (int l = 0; l <= N; ++l) *reinterpret_cast<uint32_t*>(base + (size_t)l * pr.b8_mod_stride) = 0u;
       continue;
     }
-    int q0[4], q1[4], q2[4], E[4];
-    int anyE = 0;
+    double xs[4], xt[4];
+    scaled<4>(a, sh, xs);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const double xs = mul_pow2(a[e], sh);
-      const double xt = trunc(xs);
-      const double fr = xs - xt;
+      xt[e] = trunc(xs[e]);
+      const double fr = xs[e] - xt[e];
       if (split == 0) {
         da2 = fma(fr, fr, da2);
-        na2 = fma(xt, xt, na2);
+        na2 = fma(xt[e], xt[e], na2);
       }
-      chunks(xt, q0[e], q1[e], q2[e], E[e]);
-      anyE |= E[e];
     }
     if (!write) continue;
-    const bool wE = __any(anyE != 0);
-    for (int l = 0; l < N; ++l) {
-      uint32_t q;
-      residue_bytes<4>(q0, q1, q2, E, wE, plane_c(tab, l, 0), sm.pow2[l], &q);
-      *reinterpret_cast<uint32_t*>(base + (size_t)l * pr.b8_mod_stride) = q;
-    }
+    planes<4, kWide>(xt, N, tab, 0, base, pr.b8_mod_stride);
     uint32_t q = 0u;
 #pragma unroll
     for (int e = 0; e < 4; ++e) q |= abs_u8(a[e], sg) << (8 * e);
@@ -434,6 +455,9 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
   }
 }
 
+// kWide: three-word digits (any N); the two-word kernel is launched only for calls whose every
+// problem has T_N < 1.5 2^62
+template <bool kWide>
 __global__ void __launch_bounds__(kThreads) prep_kernel(const oz2_problem* __restrict__ probs, int a_blocks,
                                                         const CrtTables* __restrict__ tab,
                                                         unsigned long long* __restrict__ cnt, int fold_q,
@@ -442,21 +466,14 @@ __global__ void __launch_bounds__(kThreads) prep_kernel(const oz2_problem* __res
   const oz2_problem& pr = probs[blockIdx.y];
   const int N = pr.num_moduli;
   if (N < 1 || N > kMaxModuli || pr.alpha == 0.0) return;   // alpha == 0: A, B never referenced
+  // folded A residues use the weights q 2^(8 i) mod p, so that sum b_i [q 2^(8 i)] = q x (mod p)
   const bool fold = fold_q && (int)blockIdx.x < a_blocks;
-  // 2^e mod p; for folded A residues (q 2^e) mod p, so that sum c_i [q 2^(E_i)] = q x (mod p)
-  for (int q = threadIdx.x; q < kMaxModuli * kPow2Table; q += kThreads) {
-    const int l = q / kPow2Table;
-    uint32_t v = tab->pow2[l][q % kPow2Table];
-    if (fold && l < N) v = (v * (uint32_t)tab->qinv[N][l]) % (uint32_t)tab->p[l];
-    (&sm.pow2[0][0])[q] = (uint8_t)v;
-  }
-  __syncthreads();
   const int blk = (int)blockIdx.x;
   if (blk < a_blocks) {
     if (blk * kARows >= pr.m) return;
-    prep_rows(pr, tab, blk, blockIdx.z, gridDim.z, sm, cnt, fold ? N : 0, packed != 0);
+    prep_rows<kWide>(pr, tab, blk, blockIdx.z, gridDim.z, sm, cnt, fold ? N : 0, packed != 0);
   } else {
-    prep_cols(pr, tab, blk - a_blocks, blockIdx.z, gridDim.z, sm, cnt, packed != 0);
+    prep_cols<kWide>(pr, tab, blk - a_blocks, blockIdx.z, gridDim.z, sm, cnt, packed != 0);
   }
 }
 
@@ -464,9 +481,10 @@ int g_force_split = 0;
 
 }  // namespace
 
-int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t s, int fold_q, int packed) {
+int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t s, int fold_q, int packed,
+                int max_moduli) {
   if (num <= 0) return 0;
-  if (num > 65535 || max_m < 0 || max_n < 0) return 1;
+  if (num > 65535 || max_m < 0 || max_n < 0 || max_moduli < 1 || max_moduli > kMaxModuli) return 1;
   DevCtx* c = dev_ctx();
   if (!c) return 2;
   const int a_blocks = (max_m + kARows - 1) / kARows;
@@ -476,15 +494,21 @@ int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t
   const long long target = 4LL * c->num_cus;
   int S = (int)std::min<long long>(16, std::max<long long>(1, (target + blocks - 1) / blocks));
   if (g_force_split > 0) S = g_force_split;
-  hipLaunchKernelGGL(prep_kernel, dim3(a_blocks + b_blocks, num, S), dim3(kThreads), 0, s, d, a_blocks,
-                     c->tab, c->counters, fold_q, packed);
+  const CrtTables* ht = host_tables();
+  if (!ht) return 2;
+  if (ht->T[max_moduli] < 0x1.8p62)
+    hipLaunchKernelGGL(prep_kernel<false>, dim3(a_blocks + b_blocks, num, S), dim3(kThreads), 0, s, d, a_blocks,
+                       c->tab, c->counters, fold_q, packed);
+  else
+    hipLaunchKernelGGL(prep_kernel<true>, dim3(a_blocks + b_blocks, num, S), dim3(kThreads), 0, s, d, a_blocks,
+                       c->tab, c->counters, fold_q, packed);
   return hipGetLastError() == hipSuccess ? 0 : 3;
 }
 
 }  // namespace ggemm
 
 extern "C" int oz2_prep_grouped(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t s) {
-  return ggemm::prep_launch(d, num, max_m, max_n, s, 0);
+  return ggemm::prep_launch(d, num, max_m, max_n, s, 0, 0, ggemm::kMaxModuli);   // N is device-side only
 }
 
 extern "C" void oz2_debug_force_prep_split(int S) { ggemm::g_force_split = (S >= 1 && S <= 64) ? S : 0; }

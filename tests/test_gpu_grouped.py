@@ -163,6 +163,21 @@ def test_config1_plumbing_fixed_n14():
     check_case(case, G.PATH_EMU_GROUPED, cfg, st, O.REPAIR_COUNT)
 
 
+@pytest.mark.parametrize("N", [16, 17, 20])
+@pytest.mark.parametrize("path", [G.PATH_EMU_GROUPED, G.PATH_EMU_LOOP])
+def test_fixed_moduli_digit_widths(path, N):
+    """Fixed N on both sides of the residue kernel's digit-width switch (two 32-bit digit words
+    of the scaled integers for N <= 16, three above), wide exponent range (phi = 2) so that
+    every row and column uses the whole norm budget; ragged k (kp = 32 mod 64)."""
+    case = Case([(96, 80, 160), (64, 72, 100), (130, 66, 33)], 20261208 + N, phi=2.0, beta=0.5)
+    cfg = G.Config(N, 1e-15, 0, 0)
+    say(f"fixed N={N} path={path}")
+    rc, st = run(case, path, cfg)
+    assert rc == 0
+    assert st.moduli_min == st.moduli_max == N
+    check_case(case, path, cfg, st, O.REPAIR_COUNT)
+
+
 @pytest.mark.parametrize("path", [G.PATH_EMU_GROUPED, G.PATH_AUTO, G.PATH_EMU_LOOP, G.PATH_EMU_LOOP_BATCHED])
 def test_uniform_group_beta(path):
     """Config-2 shape family, reduced: G=8 x 192^3, (U-0.5)exp(0.5 Z), alpha=1, beta=0.5."""
