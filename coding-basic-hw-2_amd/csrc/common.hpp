@@ -121,10 +121,12 @@ __host__ __device__ inline size_t blocked_word(int r4, int c, int mb) {
 // large-tile one (every tile 256 x 256, one 8-wave workgroup per compute unit).
 enum { kI8General = 0, kI8Large = 1 };
 // Builds the INT8 schedule (LPT order); cfg < 0 in a problem selects automatically.
-// allow_large: the large-tile kernel may be chosen (when every product is on automatic large
-// tiles and they fill the GPU); *kernel receives the choice, which i8_launch must be given.
+// large: kLargeNever, kLargeAuto (the large-tile kernel when every product is on automatic large
+// tiles and they fill the GPU) or kLargeForce (whenever every product's tile is automatic);
+// *kernel receives the choice, which i8_launch must be given.
+enum { kLargeNever = 0, kLargeAuto = 1, kLargeForce = 2 };
 int i8_build_schedule(const i8_problem* h, int num, void* h_ws, size_t ws_bytes, i8_sched_info* info,
-                      int num_cus, int allow_large = 0, int* kernel = nullptr);
+                      int num_cus, int large = kLargeNever, int* kernel = nullptr);
 // d_epi: per-problem epilogues in device memory, or nullptr for int32 products everywhere.
 int i8_launch(const i8_problem* d_probs, const I8Epi* d_epi, const void* d_sched, const i8_sched_info* info,
               hipStream_t s, int kernel = kI8General);
@@ -191,5 +193,6 @@ struct ggemm_handle_s {
   size_t *ua_off8, *ua_offs, *ub_off8, *ub_offs;
   int reuse_promote;   // GGEMM_REUSE_PROMOTE=1 at create: PROMOTE policy, else EXACT_N
   int digits_colmajor; // GGEMM_DIGITS_COLMAJOR=1 at create: row-major residues and column-major digits
+  int i8_mode;         // GGEMM_I8_KERNEL at create: 0 automatic, 1 general kernel only, 2 large-tile kernel
                        // only, the kernel-level layouts (testing)
 };

@@ -129,6 +129,15 @@ static void workspace_diag(ggemm_handle_t h, const ggemm_problem_t* probs, const
                kmin, h->min_k, kmin);
 }
 
+// INT8 kernel choice: with packed residues (every Kp small) the general kernel's two workgroups
+// per compute unit overlap one tile's epilogue with the other's MFMA work and win; with
+// row-major residues (long k) the large tiles' halved operand stream per MFMA wins.
+int large_mode(ggemm_handle_t h, const GroupedCall& c) {
+  if (h->i8_mode == 1) return kLargeNever;
+  if (h->i8_mode == 2) return kLargeForce;
+  return c.packed ? kLargeNever : kLargeAuto;
+}
+
 int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const ggemm_plan_entry_t* plan,
                   int* emu_idx, int* nat_idx, char* hb, size_t cap, GroupedCall* out, ggemm_stats_t* st,
                   const reuse_plan* rp) {
@@ -309,7 +318,8 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
   }
   for (int i = 0; i < c.nn; ++i) hf[i] = f64_of(probs[nat_idx[i]]);
   if (c.nn && f64_build_schedule(hf, c.nn, hb + c.L.off_sf64, s_f64, &c.f64_tiles, nullptr)) return GGEMM_ERR_INVALID;
-  if (c.ne && i8_build_schedule(hi8, (int)c.n_i8, hb + c.L.off_si8, s_i8, &c.i8info, h->num_cus, 1, &c.i8_kernel))
+  if (c.ne && i8_build_schedule(hi8, (int)c.n_i8, hb + c.L.off_si8, s_i8, &c.i8info, h->num_cus, large_mode(h, c),
+                                   &c.i8_kernel))
     return GGEMM_ERR_I8GEMM;
   c.h2d_bytes = c.ne ? c.L.off_si8 + c.i8info.bytes_used : c.L.off_si8;
   *out = c;
@@ -674,6 +684,8 @@ extern "C" int ggemm_create_ex(ggemm_handle_t* out, int max_problems, size_t max
   h->reuse_promote = (ep && std::atoi(ep) == 1) ? 1 : 0;
   const char* ec = std::getenv("GGEMM_DIGITS_COLMAJOR");
   h->digits_colmajor = (ec && std::atoi(ec) == 1) ? 1 : 0;
+  const char* eg = std::getenv("GGEMM_I8_KERNEL");
+  h->i8_mode = !eg ? 0 : !std::strcmp(eg, "general") ? 1 : !std::strcmp(eg, "large") ? 2 : 0;
   const char* e = std::getenv("GGEMM_STATS_REPAIR");
   h->stats_repair = (e && std::atoi(e) == 1) ? 1 : 0;
   if (hipStreamSynchronize(stream) != hipSuccess) FAIL(GGEMM_ERR_CUDA);

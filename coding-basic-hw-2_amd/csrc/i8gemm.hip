@@ -396,7 +396,7 @@ int auto_cfg(int m, int n) {
 }  // namespace
 
 int i8_build_schedule(const i8_problem* h, int num, void* h_ws, size_t ws_bytes, i8_sched_info* info, int num_cus,
-                      int allow_large, int* kernel) {
+                      int large, int* kernel) {
   if (num < 0 || (num > 0 && !h) || !h_ws || !info) return 1;
   if (ws_bytes < sched_bytes(num)) return 2;
   if (kernel) *kernel = kI8General;
@@ -411,9 +411,12 @@ int i8_build_schedule(const i8_problem* h, int num, void* h_ws, size_t ws_bytes,
     if (c >= kI8NumCfg) c = kI8NumCfg - 1;
     ents.push_back({(double)i8_tile_m(c) * i8_tile_n(c) * (double)(h[i].kp + 128), tiles_of(c, h[i].m, h[i].n), i, c});
   }
+  bool all_auto = !ents.empty();
+  for (auto& e : ents) all_auto = all_auto && h[e.prob].tile_cfg < 0;
+  const bool force_large = large == kLargeForce && all_auto;
   // group-level fill: fewer tiles than workgroup slots (2 per compute unit) -> shrink automatic
   // tiles one step
-  for (int pass = 0; pass < 2; ++pass) {
+  for (int pass = 0; pass < 2 && !force_large; ++pass) {
     long long t = 0;
     for (auto& e : ents) t += e.tiles;
     if (t >= 2LL * num_cus) break;
@@ -426,14 +429,14 @@ int i8_build_schedule(const i8_problem* h, int num, void* h_ws, size_t ws_bytes,
   }
   // large-tile kernel: every product on automatic large tiles, and enough 256 x 256 tiles to give
   // every compute unit one
-  if (allow_large && !ents.empty()) {
+  if (large != kLargeNever && !ents.empty()) {
     bool all = true;
     long long t = 0;
     for (auto& e : ents) {
       all = all && e.cfg == 0 && h[e.prob].tile_cfg < 0;
       t += (long long)((h[e.prob].m + 255) / 256) * ((h[e.prob].n + 255) / 256);
     }
-    if (all && t >= num_cus) {
+    if (force_large || (all && t >= num_cus)) {
       for (auto& e : ents) {
         e.tiles = ((h[e.prob].m + 255) / 256) * ((h[e.prob].n + 255) / 256);
         e.cost = 256.0 * 256.0 * (double)(h[e.prob].kp + 128);

@@ -189,28 +189,71 @@ def test_uniform_group_beta(path):
     check_case(case, path, cfg, st, O.REPAIR_ON if path == G.PATH_AUTO else O.REPAIR_COUNT)
 
 
-def test_large_tile_kernel_ragged_edges():
-    """Every product on automatic large tiles and enough 256 x 256 tiles to fill the GPU: the
-    pipeline takes the large-tile INT8 kernel.  m, n are not multiples of 256 (clamped edge rows)
-    and kp = 480 is 32 mod 64 (the zeroed half stage)."""
+def kernel_handle(case, kernel=None, **env):
+    """A handle created with GGEMM_I8_KERNEL (and further variables) set: read at creation."""
+    saved = dict(os.environ)
+    if kernel:
+        os.environ["GGEMM_I8_KERNEL"] = kernel
+    os.environ.update(env)
+    try:
+        return G.Handle(len(case.hp), *case.sizes())
+    finally:
+        os.environ.clear()
+        os.environ.update(saved)
+
+
+def run_kernel(case, kernel, cfg=CFG_EMU, **env):
+    """EMU_GROUPED through a handle forced onto one INT8 kernel; checks that kernel ran."""
+    with kernel_handle(case, kernel, **env) as h:
+        rc, st = run(case, G.PATH_EMU_GROUPED, cfg, handle=h)
+        assert rc == 0
+        want = {"large": "i8_large_kernel", "general": "i8_grouped_kernel"}[kernel]
+        assert G.lib().ggemm_profile_i8_kernel().decode() == want
+        check_case(case, G.PATH_EMU_GROUPED, cfg, st, O.REPAIR_COUNT)
+        return [case.C(g).copy() for g in range(len(case.hp))]
+
+
+@pytest.mark.parametrize("kernel", ["large", "general"])
+def test_large_tile_kernel_ragged_edges(kernel):
+    """The large-tile INT8 kernel (forced with GGEMM_I8_KERNEL; by default it serves long-k
+    calls) and the general kernel on the same products: m, n are not multiples of 256 (clamped
+    edge rows) and kp = 480 is 32 mod 64 (the zeroed half stage)."""
     case = Case([(520, 600, 470)] * 3, 20261206, phi=0.5, beta=0.5)
-    say("large-tile kernel, ragged edges")
-    rc, st = run(case, G.PATH_EMU_GROUPED, CFG_EMU)
-    assert rc == 0
-    check_case(case, G.PATH_EMU_GROUPED, CFG_EMU, st, O.REPAIR_COUNT)
+    say(f"{kernel} kernel, ragged edges")
+    run_kernel(case, kernel)
 
 
-def test_large_tile_kernel_mixed_k_stream():
-    """The large-tile kernel keeps one workgroup per compute unit and streams k-stages across
-    its tiles: products with 1 to 9 k-stages (kp = 64 .. 576, some 32 mod 64) follow each other
-    in one workgroup's ring, with full tiles (exact stores) and a ragged n (edge stores)."""
+@pytest.mark.parametrize("colmajor", [False, True])
+def test_large_tile_kernel_mixed_k_stream(colmajor):
+    """The large-tile kernel on products with 1 to 9 k-stages (kp = 64 .. 576, some 32 mod 64),
+    full tiles and a ragged n (edge stores), with the packed residues and blocked digits and with
+    the row-major / column-major layouts (GGEMM_DIGITS_COLMAJOR=1)."""
     shapes = [(512, 512, 40), (512, 512, 64), (512, 512, 100), (512, 512, 160),
               (512, 520, 300), (512, 512, 520), (512, 512, 576)]
     case = Case(shapes, 20261207, phi=0.5, beta=0.5)
-    say("large-tile kernel, mixed k stream")
-    rc, st = run(case, G.PATH_EMU_GROUPED, CFG_EMU)
-    assert rc == 0
-    check_case(case, G.PATH_EMU_GROUPED, CFG_EMU, st, O.REPAIR_COUNT)
+    say(f"large-tile kernel, mixed k stream, colmajor={colmajor}")
+    run_kernel(case, "large", **({"GGEMM_DIGITS_COLMAJOR": "1"} if colmajor else {}))
+
+
+def test_default_kernel_choice():
+    """Automatic choice: the general kernel for calls with packed residues (every Kp <= 4096),
+    the large-tile kernel for long-k calls whose 256 x 256 tiles fill the GPU."""
+    say("default kernel choice")
+    short = Case([(256, 256, 300)] * 2, 20261209, phi=0.5)
+    with kernel_handle(short) as h:
+        rc, st = run(short, G.PATH_EMU_GROUPED, CFG_EMU, handle=h)
+        assert rc == 0 and G.lib().ggemm_profile_i8_kernel().decode() == "i8_grouped_kernel"
+    props = torch.cuda.get_device_properties(0)
+    g = (props.multi_processor_count + 3) // 4      # 4 tiles of 256 x 256 per problem
+    long_k = Case([(512, 512, 4128)] * g, 20261210, phi=0.5)   # kp = 4128 > 4096: row-major
+    outs = []
+    for kernel, name in ((None, "i8_large_kernel"), ("general", "i8_grouped_kernel")):
+        with kernel_handle(long_k, kernel) as h:
+            rc, st = run(long_k, G.PATH_EMU_GROUPED, CFG_EMU, handle=h)
+            assert rc == 0 and G.lib().ggemm_profile_i8_kernel().decode() == name
+            outs.append([long_k.C(q).copy() for q in range(g)])
+    for a, b in zip(*outs):   # the oracle checks both kernels on smaller shapes above
+        assert same_bits(a, b)
 
 
 @pytest.mark.parametrize("shapes", [[(300, 270, 200)] * 2 + [(17, 33, 90), (64, 48, 40)],   # general kernel
@@ -222,20 +265,9 @@ def test_blocked_and_columnmajor_digits_same_bits(shapes):
     column-major digits; GGEMM_DIGITS_COLMAJOR=1 forces them).  Both give the oracle's bits; m, n
     are not multiples of 16 (padded blocks) and kp = 96, 224, 480 end in a 32-byte half block."""
     case = Case(shapes, 20261208, phi=0.5, beta=0.5)
-    say("blocked vs column-major digits")
-    outs = []
-    for colmajor in (False, True):
-        if colmajor:
-            os.environ["GGEMM_DIGITS_COLMAJOR"] = "1"
-        try:
-            h = G.Handle(len(shapes), *case.sizes())
-        finally:
-            os.environ.pop("GGEMM_DIGITS_COLMAJOR", None)
-        with h:
-            rc, st = run(case, G.PATH_EMU_GROUPED, CFG_EMU, handle=h)
-            assert rc == 0
-            check_case(case, G.PATH_EMU_GROUPED, CFG_EMU, st, O.REPAIR_COUNT)
-            outs.append([case.C(g).copy() for g in range(len(shapes))])
+    kernel = "large" if len(shapes) == 3 else "general"
+    say(f"blocked vs column-major digits, {kernel} kernel")
+    outs = [run_kernel(case, kernel), run_kernel(case, kernel, GGEMM_DIGITS_COLMAJOR="1")]
     for a, b in zip(*outs):
         assert same_bits(a, b)
 
