@@ -83,11 +83,15 @@ constexpr int kI8NumCfg = 3;
 __host__ __device__ inline int i8_tile_m(int cfg) { return cfg == 0 ? 256 : (cfg == 1 ? 128 : 64); }
 __host__ __device__ inline int i8_tile_n(int cfg) { return cfg == 0 ? 128 : (cfg == 1 ? 128 : 64); }
 // Per-product epilogue of the INT8 GEMM, mode bits:
-//   kEpiResidue  one byte per entry, the residue C mod p in [0, p), from u = C + bias in [0, 2^32)
-//                (bias = p ceil(2^31 / p)) by a Barrett step with mc = ceil(2^32 / p) and one
-//                correction; without it the int32 product.  In the production pipeline the A
-//                residues of plane l carry the CRT inverse q_l (prep with fold_q), so this byte
-//                is the CRT digit y_l = (C_l q_l) mod p_l.
+//   kEpiResidue  one byte per entry, the residue C mod p in [0, p), from u = C + bias >= 0
+//                by a Barrett step q = umulhi(u, mc), mc = ceil(2^32 / p) (q = floor(u / p) or one
+//                more), r = u - q p in [-p, p) and one correction; without it the int32 product.
+//                In the production pipeline the A residues of plane l carry the CRT inverse q_l
+//                (prep with fold_q), so this byte is the CRT digit y_l = (C_l q_l) mod p_l.
+//   kEpiAccBias  (with kEpiResidue, kp <= 32768) bias = p ceil(2^29 / p) >= |C| is the MFMA
+//                accumulators' initial value, so u is the accumulator itself, u < 2^30 + p,
+//                q < 2^23 and r = u - q p is one 24-bit multiply-add; otherwise (long k)
+//                bias = p ceil(2^31 / p), u = C + bias < 2^32 and r takes a 32-bit multiply.
 //   kEpiBlocked  16 x 16 blocked output (below) instead of column-major with ld m.
 // Blocked layout of an m x n plane: blocks (bi, bj) of 16 x 16 entries in column-major block
 // order (MB = ceil(m / 16) block rows), each block stored as one MFMA result block: lane
@@ -99,7 +103,8 @@ __host__ __device__ inline int i8_tile_n(int cfg) { return cfg == 0 ? 128 : (cfg
 // of 64 bytes, block b holding the bytes k in [64 b, 64 b + 64) of every row contiguously
 // ([b][row][64]); with Kp % 64 == 32 the last block holds 32 bytes per row.  A 64-byte k-stage of
 // consecutive rows is then one contiguous span.
-enum : uint32_t { kEpiResidue = 1u, kEpiBlocked = 2u, kEpiPacked = 4u };
+enum : uint32_t { kEpiResidue = 1u, kEpiBlocked = 2u, kEpiPacked = 4u, kEpiAccBias = 8u };
+constexpr int kAccBiasMaxKp = 32768;   // |C| <= 128^2 kp <= 2^29
 constexpr int kPackedMaxKp = 4096;   // production calls whose largest Kp is at most this use packing
 __host__ __device__ inline size_t packed_offset(int row, int k, int rows, int kp) {
   const int b = k >> 6;
@@ -109,7 +114,7 @@ __host__ __device__ inline size_t packed_offset(int row, int k, int rows, int kp
 struct I8Epi {
   uint32_t mode, p, mc, bias;
 };
-I8Epi i8_epi_residue(uint32_t p);
+I8Epi i8_epi_residue(uint32_t p, int kp);
 __host__ __device__ inline size_t blocked_plane_entries(int m, int n) {
   return (size_t)((m + 15) / 16) * (size_t)((n + 15) / 16) * 256;
 }

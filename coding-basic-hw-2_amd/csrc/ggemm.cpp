@@ -273,7 +273,7 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
       d.tile_cfg = -1;
       if (l < N) {
         d.C = reinterpret_cast<int32_t*>(ybase + oy + (size_t)l * SY);
-        hepi[q] = i8_epi_residue((uint32_t)tab->p[l]);   // A residues carry q_l: the byte is y_l
+        hepi[q] = i8_epi_residue((uint32_t)tab->p[l], (int)kp);   // A residues carry q_l: the byte is y_l
       } else {
         d.C = lbase + ol;
         hepi[q] = I8Epi{0u, 1u, 0u, 0u};

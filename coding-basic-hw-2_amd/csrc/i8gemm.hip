@@ -156,13 +156,50 @@ __device__ __forceinline__ void dma_stage(const StageSrc& a, const StageSrc& b, 
   }
 }
 
-// C mod p in [0, p): u = C + bias in [0, 2^32) (bias = p ceil(2^31 / p)), q = umulhi(u, mc) with
-// mc = ceil(2^32 / p) is floor(u / p) or one more (u (mc - 2^32/p) < 2^32), r = u - q p, plus p
-// when that is negative.
+// C mod p in [0, p) from u = C + bias >= 0: q = umulhi(u, mc) with mc = ceil(2^32 / p) is floor(u / p)
+// or one more (u (mc - 2^32/p) < 2^32), so r = u - q p is in [-p, p), and min(r, r + p) as unsigned
+// is r mod p.  kAcc: u is the accumulator (it started at the bias), u < 2^30 + p and q < 2^23, so
+// r is one 24-bit multiply-add.
+template <bool kAcc>
 __device__ __forceinline__ uint32_t residue_byte(int32_t c, const I8Epi& e) {
-  const uint32_t u = (uint32_t)c + e.bias;
-  const int r = (int)(u - __umulhi(u, e.mc) * e.p);
-  return (uint32_t)(r + (r < 0 ? (int)e.p : 0));
+  const uint32_t u = kAcc ? (uint32_t)c : (uint32_t)c + e.bias;
+  const uint32_t q = __umulhi(u, e.mc);
+  const int r = kAcc ? __mul24((int)q, -(int)e.p) + (int)u : (int)(u - q * e.p);
+  return min((uint32_t)r, (uint32_t)(r + (int)e.p));
+}
+
+// Blocked epilogue: kind 0 int32 blocks (16 bytes per lane), 1 residue bytes from biased
+// accumulators, 2 residue bytes with the bias added here (4 bytes per lane, packed with v_perm).
+// The block offsets are wave-uniform; a lane writes at 4 lane entries into each block.
+template <class C>
+__device__ __forceinline__ void store_blocked(const v4i (&acc)[C::FM][C::FN], const i8_problem& P, const I8Epi& epi,
+                                              int kind, int bi0, int bj0, int mb, int lane) {
+  uint8_t* const y8 = reinterpret_cast<uint8_t*>(P.C) + 4 * lane;
+  int32_t* const y32 = reinterpret_cast<int32_t*>(P.C) + 4 * lane;
+#pragma unroll
+  for (int j = 0; j < C::FN; ++j)
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i) {
+      const int bi = bi0 + i, bj = bj0 + j;
+      if (bi * 16 >= P.m || bj * 16 >= P.n) continue;   // wave-uniform
+      const size_t e0 = ((size_t)bj * mb + bi) * 256;
+      const v4i v = acc[i][j];
+      if (kind == 0) {
+        *reinterpret_cast<v4i*>(y32 + e0) = v;
+      } else {
+        uint32_t y[4];
+        if (kind == 1) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) y[r] = residue_byte<true>(v[r], epi);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) y[r] = residue_byte<false>(v[r], epi);
+        }
+        const uint32_t lo = __builtin_amdgcn_perm(y[1], y[0], 0x0c0c0400u);
+        const uint32_t hi = __builtin_amdgcn_perm(y[3], y[2], 0x0c0c0400u);
+        *reinterpret_cast<uint32_t*>(y8 + e0) = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+      }
+    }
 }
 
 template <class C, bool kPacked>
@@ -187,16 +224,19 @@ __device__ __forceinline__ void run_tile(uint8_t* lds, const i8_problem& P, cons
   const uint32_t a_addr = lbase + ra * kBK + swz(ra, fc) * 16;
   const uint32_t b_addr = lbase + rb * kBK + swz(rb, fc) * 16;
 
+  const int a0 = (epi.mode & kEpiAccBias) ? (int)epi.bias : 0;   // accumulator start
   v4i acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < FN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+    for (int j = 0; j < FN; ++j) acc[i][j] = v4i{a0, a0, a0, a0};
 
 #pragma unroll
   for (int q = 0; q < NST - 1; ++q)
     if (q < nk) load(q, lds + q * C::STAGE);
   int buf = 0;
+  if (nk <= 0) return;      // never scheduled: problems with kp == 0 get no tiles
+  __builtin_assume(nk > 0);  // one path into the epilogue (no zero-trip copy of the accumulators)
   for (int kt = 0; kt < nk; ++kt) {
     // stage kt landed (the NST - 2 stages after it may still be in flight; near the end fewer
     // were issued, so wait for everything) and every wave is done with stage kt - 1
@@ -231,24 +271,12 @@ __device__ __forceinline__ void run_tile(uint8_t* lds, const i8_problem& P, cons
   // 64 lanes' values are one 16 x 16 block of the blocked output layout.
   const bool residue = (epi.mode & kEpiResidue) != 0;
   if (epi.mode & kEpiBlocked) {   // every existing block is stored whole (padding included)
+    // block (bi, bj) of the wave: uniform offset (bj MB + bi) 256 entries, lane l at entries 4 l
     const int mb = (P.m + 15) / 16;
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const int br = row0 + wm * C::WM + i * 16, bc = col0 + wn * C::WN + j * 16;
-        if (br >= P.m || bc >= P.n) continue;
-        const size_t w = blocked_word(br + 4 * (lane >> 4), bc + (lane & 15), mb);
-        const v4i v = acc[i][j];
-        if (residue) {
-          uint32_t y[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) y[r] = residue_byte(v[r], epi);
-          *reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(P.C) + w) = y[0] | (y[1] << 8) | (y[2] << 16) | (y[3] << 24);
-        } else {
-          *reinterpret_cast<v4i*>(reinterpret_cast<int32_t*>(P.C) + w) = v;
-        }
-      }
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    const int bi0 = (row0 + (wv % C::WGM) * C::WM) / 16, bj0 = (col0 + (wv / C::WGM) * C::WN) / 16;
+    const int kind = !residue ? 0 : (epi.mode & kEpiAccBias) ? 1 : 2;
+    store_blocked<C>(acc, P, epi, kind, bi0, bj0, mb, lane);
     return;
   }
   const size_t ldc = (size_t)P.m;
@@ -274,7 +302,7 @@ __device__ __forceinline__ void run_tile(uint8_t* lds, const i8_problem& P, cons
         uint8_t* out = reinterpret_cast<uint8_t*>(P.C) + (size_t)r0 + (size_t)col * ldc;
         uint32_t y[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) y[r] = residue_byte(v[r], epi);
+        for (int r = 0; r < 4; ++r) y[r] = (epi.mode & kEpiAccBias) ? residue_byte<true>(v[r], epi) : residue_byte<false>(v[r], epi);
         if (vec && r0 + 3 < P.m) {
           *reinterpret_cast<uint32_t*>(out) = y[0] | (y[1] << 8) | (y[2] << 16) | (y[3] << 24);
         } else {
@@ -474,8 +502,10 @@ int i8_build_schedule(const i8_problem* h, int num, void* h_ws, size_t ws_bytes,
   return 0;
 }
 
-I8Epi i8_epi_residue(uint32_t p) {
-  return I8Epi{kEpiResidue, p, (uint32_t)((4294967296ull + p - 1) / p), p * (uint32_t)((2147483648ull + p - 1) / p)};
+I8Epi i8_epi_residue(uint32_t p, int kp) {
+  const uint32_t mc = (uint32_t)((4294967296ull + p - 1) / p);
+  if (kp <= kAccBiasMaxKp) return I8Epi{kEpiResidue | kEpiAccBias, p, mc, p * (((1u << 29) + p - 1) / p)};
+  return I8Epi{kEpiResidue, p, mc, p * (uint32_t)((2147483648ull + p - 1) / p)};
 }
 
 namespace {

@@ -135,3 +135,40 @@ def test_two_word_layout_range():
     # two words: |x| <= T_N and x + 2^32 H-bias must not wrap: T_N < 1.5 2^62 exactly for N <= 16
     assert [N for N in range(1, 21) if _T(N) < 1.5 * 2.0 ** 62] == list(range(1, 17))
     assert _T(20) < 2.0 ** 77
+
+
+# ------------------------------------------------------------------- INT8 GEMM epilogue (i8gemm.hip)
+def _epi_params(p, kp):
+    mc = -(-(1 << 32) // p)
+    if kp <= 32768:
+        return mc, p * -(-(1 << 29) // p), True
+    return mc, p * -(-(1 << 31) // p), False
+
+
+def _epi_byte(c, p, kp):
+    """The epilogue's C mod p from the int32 product c (uint32 / int32 wrap emulated)."""
+    mc, bias, acc = _epi_params(p, kp)
+    u = (c + bias) & 0xFFFFFFFF
+    q = (u * mc) >> 32
+    if acc:
+        assert q < 1 << 23 and u < (1 << 31)   # 24-bit multiply-add operand, non-negative int32 accumulator
+        r = u - q * p
+    else:
+        r = (u - q * p) & 0xFFFFFFFF
+        r = r - (1 << 32) if r >= 1 << 31 else r
+    assert -p <= r < p
+    return min(r & 0xFFFFFFFF, (r + p) & 0xFFFFFFFF)
+
+
+@pytest.mark.parametrize("kp", [32, 1024, 32768, 32800, 131040])
+def test_gemm_epilogue_residue(kp):
+    cmax = 128 * 128 * kp   # |C| <= 128^2 kp for residues in [-128, 127]
+    rng = np.random.default_rng(kp)
+    for p in MODULI:
+        cs = set(int(v) for v in rng.integers(-cmax, cmax + 1, 2000))
+        for base in (0, cmax, -cmax, 1 << 20, -(1 << 20)):
+            for d in range(-2 * p, 2 * p + 1):
+                if -cmax <= base + d <= cmax:
+                    cs.add(base + d)
+        for c in cs:
+            assert _epi_byte(c, p, kp) == c % p, (c, p, kp)
