@@ -156,6 +156,27 @@ __device__ __forceinline__ void dma_stage(const StageSrc& a, const StageSrc& b, 
   }
 }
 
+// The same stage when every row of the tile exists and every chunk is inside the row (the common
+// case): piece offsets are wave-uniform and the per-lane offset r_in stride + 16 swz(r_in, pc) is
+// fixed for the tile (the swizzle of row 16 piece + r_in depends on r_in only), so each DMA is a
+// scalar base plus one per-lane offset.
+template <class C>
+__device__ __forceinline__ void dma_stage_full(const int8_t* a, const int8_t* b, int a_stride, int b_stride,
+                                               uint32_t a_lane, uint32_t b_lane, uint8_t* st, int wave) {
+#pragma unroll
+  for (int q = 0; q < C::DA; ++q) {
+    const int piece = wave + C::NW * q;
+    __builtin_amdgcn_global_load_lds((const void*)(a + (size_t)piece * 16 * a_stride + a_lane),
+                                     GGEMM_LDS(st + piece * 1024), 16, 0, 0);
+  }
+#pragma unroll
+  for (int q = 0; q < C::DB; ++q) {
+    const int piece = wave + C::NW * q;
+    __builtin_amdgcn_global_load_lds((const void*)(b + (size_t)piece * 16 * b_stride + b_lane),
+                                     GGEMM_LDS(st + C::SA + piece * 1024), 16, 0, 0);
+  }
+}
+
 // C mod p in [0, p) from u = C + bias >= 0: q = umulhi(u, mc) with mc = ceil(2^32 / p) is floor(u / p)
 // or one more (u (mc - 2^32/p) < 2^32), so r = u - q p is in [-p, p), and min(r, r + p) as unsigned
 // is r mod p.  kAcc: u is the accumulator (it started at the bias), u < 2^30 + p and q < 2^23, so
@@ -205,15 +226,28 @@ __device__ __forceinline__ void store_blocked(const v4i (&acc)[C::FM][C::FN], co
 template <class C, bool kPacked>
 __device__ __forceinline__ void run_tile(uint8_t* lds, const i8_problem& P, const I8Epi& epi, int tm, int tn) {
   constexpr int FM = C::FM, FN = C::FN, NST = C::NST;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave % C::WGM, wn = wave / C::WGM;
   const int row0 = tm * C::BM, col0 = tn * C::BN;
   const int m_rem = P.m - row0, n_rem = P.n - col0;
   const int kp = P.kp;
   const int nk = (kp + kBK - 1) / kBK;
+  // full stages: all tile rows exist and the stage has 64 bytes per row (packed: every k-block but
+  // a final half block; row-major: every stage but a final half stage)
+  const bool full_rows = m_rem >= C::BM && n_rem >= C::BN;
+  const int fstride = kPacked ? 64 : kp;
+  const int r_in = lane >> 2;
+  const uint32_t lane_off = (uint32_t)(r_in * fstride + 16 * swz(r_in, lane & 3));
   auto load = [&](int kt, uint8_t* st) {
-    dma_stage<C>(stage_src(P.A, P.m, row0, kp, kt * kBK, kPacked), stage_src(P.B, P.n, col0, kp, kt * kBK, kPacked),
-                 m_rem, n_rem, st, wave, lane);
+    const int k0 = kt * kBK;
+    if (full_rows && k0 + kBK <= kp) {
+      const int8_t* a = kPacked ? P.A + (size_t)(k0 >> 6) * P.m * 64 + (size_t)row0 * 64 : P.A + (size_t)row0 * kp + k0;
+      const int8_t* b = kPacked ? P.B + (size_t)(k0 >> 6) * P.n * 64 + (size_t)col0 * 64 : P.B + (size_t)col0 * kp + k0;
+      dma_stage_full<C>(a, b, fstride, fstride, lane_off, lane_off, st, wave);
+    } else {
+      dma_stage<C>(stage_src(P.A, P.m, row0, kp, k0, kPacked), stage_src(P.B, P.n, col0, kp, k0, kPacked), m_rem,
+                   n_rem, st, wave, lane);
+    }
   };
 
   // fragment addresses: rows wm WM + 16 i + lane % 16 (A), wn WN + 16 j + lane % 16 (B), chunk lane / 16;
