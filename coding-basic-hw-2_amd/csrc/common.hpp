@@ -123,7 +123,7 @@ __host__ __device__ inline size_t blocked_word(int r4, int c, int mb) {
   return ((size_t)(c >> 4) * (size_t)mb + (size_t)(r4 >> 4)) * 256 + (size_t)(16 * ((r4 & 15) >> 2) + (c & 15)) * 4;
 }
 // INT8 GEMM kernels: the general one (tile configs 0..2, two workgroups per compute unit) and the
-// large-tile one (every tile 256 x 256, one 8-wave workgroup per compute unit).
+// large-tile one (every tile 256 x 256, one 16-wave workgroup per compute unit).
 enum { kI8General = 0, kI8Large = 1 };
 // Builds the INT8 schedule (LPT order); cfg < 0 in a problem selects automatically.
 // large: kLargeNever, kLargeAuto (the large-tile kernel when every product is on automatic large

@@ -75,8 +75,9 @@ using Cfg2 = Cfg<64, 64, 2, 2, 3>;
 constexpr int kThreads = 256;
 constexpr int kSmem = Cfg0::SMEM;
 static_assert(Cfg1::SMEM <= kSmem && Cfg2::SMEM <= kSmem, "smem");
-// large-tile kernel: 512 threads, one workgroup per compute unit, 128 KB ring
-using CfgL = Cfg<256, 256, 2, 4, 4>;
+// large-tile kernel: 1024 threads = 16 waves of 64 x 64 (4 per SIMD, so one wave's LDS reads and
+// barrier waits overlap the others' MFMAs), one workgroup per compute unit, 128 KB ring
+using CfgL = Cfg<256, 256, 4, 4, 4>;
 constexpr int kThreadsL = CfgL::NT;
 constexpr int kSmemL = CfgL::SMEM;
 
