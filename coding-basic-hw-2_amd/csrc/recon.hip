@@ -81,17 +81,19 @@ struct Counts {
   unsigned uncert, repair, safety;
 };
 
-// One entry: CRT, scaling, alpha/beta, certificate, repair.  c0 is read only when beta != 0.
+// One entry: CRT, scaling, alpha/beta, certificate.  Entries that need the FP64 dot product
+// (safety fallback, repair) return with dot set; the caller computes it.  c0 is read only when
+// beta != 0.
 __device__ __forceinline__ double entry(const oz2_problem& pr, const CrtTables* __restrict__ tab, int N, int mode,
                                         int i, int j, uint64_t S1, uint32_t S2, int32_t L, int rsh, int csh,
                                         int sig, int tau, double da, double na, double db, double nb, double c0,
-                                        double gam, Counts& cn) {
+                                        double gam, Counts& cn, bool& dot) {
   const double alpha = pr.alpha, beta = pr.beta;
   if (alpha == 0.0) return (beta == 0.0) ? 0.0 : beta * c0;   // BLAS: A, B, workspace not referenced
   if (rsh == OZ2_SHIFT_NONFINITE || csh == OZ2_SHIFT_NONFINITE) {   // safety fallback
-    const double d = fp64_dot(pr, i, j);
     ++cn.safety;
-    return (beta == 0.0) ? alpha * d : fma(alpha, d, beta * c0);
+    dot = true;
+    return 0.0;
   }
   if (sig == OZ2_SHIFT_ZERO || tau == OZ2_SHIFT_ZERO)   // zero row / column: AB_ij = 0
     return (beta == 0.0) ? alpha * 0.0 : fma(alpha, 0.0, beta * c0);
@@ -123,8 +125,89 @@ __device__ __forceinline__ double entry(const oz2_problem& pr, const CrtTables* 
     return emu;
   }
   ++cn.repair;
-  const double d = fp64_dot(pr, i, j);
+  dot = true;
+  return 0.0;
+}
+// C from the FP64 dot product d (safety fallback and repair)
+__device__ __forceinline__ double from_dot(double alpha, double beta, double d, double c0) {
   return (beta == 0.0) ? alpha * d : fma(alpha, d, beta * c0);
+}
+
+constexpr int kKC = 16;        // k-chunk of the tile dot products
+constexpr int kTileDots = 8;   // threads needing dot products from which the tile computes them all
+constexpr int kWaveDots = 4;   // lanes needing dot products from which a wave computes its whole block
+
+// Blocked layout: the same for one wave's 16 x 16 block (rows wr0 .., columns wc0 ..; lane
+// l = 16 q + c owns rows 4 q .. 4 q + 3 of column c), staged through the wave's own LDS: no
+// workgroup barrier, so waves without such entries never wait.  The wave barrier and fences order
+// the lanes' LDS writes before other lanes read them.
+__device__ __forceinline__ void wave_dots(const oz2_problem& pr, int wr0, int wc0, int lane, double* wA, double* wB,
+                                          double (&acc)[4]) {
+  const GLOBAL double* A = gp(pr.A);
+  const GLOBAL double* B = gp(pr.B);
+  const size_t lda = (size_t)pr.lda, ldb = (size_t)pr.ldb;
+  const int m = pr.m, n = pr.n, K = pr.k;
+  const int q4 = 4 * (lane >> 4), c = lane & 15;
+  const int sk = lane >> 2, sr = 4 * (lane & 3);   // staging: k-row sk, rows / k sr .. sr + 3
+#pragma unroll
+  for (int e = 0; e < 4; ++e) acc[e] = 0.0;
+  for (int kc = 0; kc < K; kc += kKC) {
+    const int kn = min(kKC, K - kc);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {   // A: wA[kk][r] (16 x 16), B: wB[col][kk] (16 x 17)
+      const int r = wr0 + sr + e, kb = kc + sr + e;
+      wA[sk * 16 + sr + e] = (r < m && sk < kn) ? A[(size_t)r + (size_t)(kc + sk) * lda] : 0.0;
+      wB[sk * (kKC + 1) + sr + e] = (wc0 + sk < n && sr + e < kn) ? B[(size_t)kb + (size_t)(wc0 + sk) * ldb] : 0.0;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll 4
+    for (int kk = 0; kk < kn; ++kk) {
+      const double b = wB[c * (kKC + 1) + kk];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] = fma(wA[kk * 16 + q4 + e], b, acc[e]);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+}
+
+// Sequential-fma dot products of every entry of an RM x CN tile (rows r0.., columns cb..), each
+// thread its rows lr .. lr + 3 of column lc: k-chunks of A (kKC x RM, rows contiguous) and B
+// (CN x kKC, padded rows against bank conflicts) staged in LDS; acc[e] = fma(a_k, b_k, acc[e]) in
+// ascending k from 0, exactly fp64_dot's chain.  Rows / columns past the problem load zeros.
+template <int RM, int CN>
+__device__ __forceinline__ void tile_dots(const oz2_problem& pr, int r0, int cb, int lr, int lc, double* tA,
+                                          double* tB, double (&acc)[4]) {
+  const GLOBAL double* A = gp(pr.A);
+  const GLOBAL double* B = gp(pr.B);
+  const size_t lda = (size_t)pr.lda, ldb = (size_t)pr.ldb;
+  const int m = pr.m, n = pr.n, K = pr.k;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) acc[e] = 0.0;
+  for (int kc = 0; kc < K; kc += kKC) {
+    const int kn = min(kKC, K - kc);
+#pragma unroll 1
+    for (int x = threadIdx.x; x < kKC * RM; x += kThreads) {
+      const int kk = x / RM, r = x % RM;
+      tA[x] = (r0 + r < m && kk < kn) ? A[(size_t)(r0 + r) + (size_t)(kc + kk) * lda] : 0.0;
+    }
+#pragma unroll 1
+    for (int x = threadIdx.x; x < CN * kKC; x += kThreads) {
+      const int c = x / kKC, kk = x % kKC;
+      tB[c * (kKC + 1) + kk] = (cb + c < n && kk < kn) ? B[(size_t)(kc + kk) + (size_t)(cb + c) * ldb] : 0.0;
+    }
+    __syncthreads();
+#pragma unroll 4
+    for (int kk = 0; kk < kn; ++kk) {
+      const double b = tB[lc * (kKC + 1) + kk];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] = fma(tA[kk * RM + lr + e], b, acc[e]);
+    }
+    __syncthreads();
+  }
 }
 
 template <bool kDigits, bool kBlocked>
@@ -137,27 +220,31 @@ __global__ void __launch_bounds__(kThreads) recon_kernel(const oz2_problem* __re
   const int N = pr.num_moduli;
   const int m = pr.m, n = pr.n, K = pr.k;
   Counts cn{0u, 0u, 0u};
-  int i0, j;
+  constexpr int RM = kBlocked ? kBTileM : kTileM, CN = kBlocked ? kBTileN : kTileN;   // tile rows, columns
+  // dot products' k-chunks: per wave (blocked layout) or for the whole tile
+  __shared__ double tA[kBlocked ? 4 * 16 * kKC : kKC * RM], tB[kBlocked ? 4 * 16 * (kKC + 1) : CN * (kKC + 1)];
+  const int tiles_m = (m + RM - 1) / RM;
+  const int r0 = ((int)blockIdx.x % max(tiles_m, 1)) * RM, cb = ((int)blockIdx.x / max(tiles_m, 1)) * CN;
+  int lr, lc;   // the thread's rows lr .. lr + 3 and column lc inside the tile
   if (kBlocked) {   // a wave per 16 x 16 block, lane = the block's MFMA lane: 4 rows of one column
-    const int tiles_m = (m + kBTileM - 1) / kBTileM;
-    const int tm = (int)blockIdx.x % max(tiles_m, 1), tn = (int)blockIdx.x / max(tiles_m, 1);
     const int lane = threadIdx.x & 63;
-    i0 = tm * kBTileM + 16 * (threadIdx.x >> 6) + 4 * (lane >> 4);
-    j = tn * kBTileN + (lane & 15);
+    lr = 16 * (threadIdx.x >> 6) + 4 * (lane >> 4);
+    lc = lane & 15;
   } else {
-    const int tiles_m = (m + kTileM - 1) / kTileM;
-    const int tm = (int)blockIdx.x % max(tiles_m, 1), tn = (int)blockIdx.x / max(tiles_m, 1);
-    i0 = tm * kTileM + 4 * (threadIdx.x & 31);
-    j = tn * kTileN + (threadIdx.x >> 5);
+    lr = 4 * (threadIdx.x & 31);
+    lc = threadIdx.x >> 5;
   }
+  const int i0 = r0 + lr, j = cb + lc;
   const bool active = N >= 1 && N <= kMaxModuli && m > 0 && n > 0 && i0 < m && j < n;
+  const double alpha = pr.alpha, beta = pr.beta;
+  const int ne = active ? min(4, m - i0) : 0;
+  const bool full = ne == 4 && (m & 3) == 0;
+  GLOBAL double* const cp = gpw(pr.C) + (active ? i0 + (size_t)j * pr.ldc : 0);
+  unsigned dmask = 0;   // entries that take the FP64 dot product
   if (active) {
-    const double alpha = pr.alpha, beta = pr.beta;
-    const int ne = min(4, m - i0);
-    const bool full = ne == 4 && (m & 3) == 0;
-    // ---- loads
-    GLOBAL double* cp = gpw(pr.C) + i0 + (size_t)j * pr.ldc;
     double c0[4] = {0.0, 0.0, 0.0, 0.0};
+    double out[4];
+    // ---- loads
     if (beta != 0.0) {
       if (full && ((reinterpret_cast<uintptr_t>(cp) & 15) == 0)) {
         const v2d a = *reinterpret_cast<const GLOBAL v2d*>(cp);
@@ -257,18 +344,51 @@ __global__ void __launch_bounds__(kThreads) recon_kernel(const oz2_problem* __re
     const double nt = (double)K + (alpha != 1.0 ? 1.0 : 0.0) + (beta != 0.0 ? 1.0 : 0.0);
     const double gam = (nt * u / (1.0 - nt * u) - 2.0 * u) * (1.0 - 0x1p-40);
     const double db = __int_as_float(dbb), nb = __int_as_float(nbb);
-    double out[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-      if (e < ne)
+      if (e < ne) {
+        bool dot = false;
         out[e] = entry(pr, tab, N, mode, i0 + e, j, S1[e], S2[e], Lv[e], rsh[e], csh, sig[e], tau,
-                       __int_as_float(dab[e]), __int_as_float(nab[e]), db, nb, c0[e], gam, cn);
-    if (full && ((reinterpret_cast<uintptr_t>(cp) & 15) == 0)) {
+                       __int_as_float(dab[e]), __int_as_float(nab[e]), db, nb, c0[e], gam, cn, dot);
+        dmask |= dot ? 1u << e : 0u;
+      }
+    // certified entries now; entries taking the dot product keep C0 in C until then
+    if (dmask == 0u && full && ((reinterpret_cast<uintptr_t>(cp) & 15) == 0)) {
       *reinterpret_cast<GLOBAL v2d*>(cp) = v2d{out[0], out[1]};
       *reinterpret_cast<GLOBAL v2d*>(cp + 2) = v2d{out[2], out[3]};
     } else {
-      for (int e = 0; e < ne; ++e) cp[e] = out[e];
+      for (int e = 0; e < ne; ++e)
+        if (!((dmask >> e) & 1u)) cp[e] = out[e];
     }
+  }
+  // ---- FP64 dot products (sequential fma over k, the reference's fp64_dot order): one per entry
+  // when few lanes need them, else a whole block / tile at once through LDS k-chunks (every lane
+  // helps; values identical, since each entry is still one fma chain in ascending k).  Blocked
+  // layout: per wave, without a workgroup barrier; column-major: per workgroup.
+  bool many;
+  if (kBlocked) {
+    many = __popcll(__ballot(dmask != 0u)) >= kWaveDots;
+    if (many) {
+      const int w = threadIdx.x >> 6;
+      double acc[4];
+      wave_dots(pr, r0 + 16 * w, cb, threadIdx.x & 63, tA + w * 16 * kKC, tB + w * 16 * (kKC + 1), acc);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if ((dmask >> e) & 1u) cp[e] = from_dot(alpha, beta, acc[e], beta != 0.0 ? cp[e] : 0.0);
+    }
+  } else {
+    many = __syncthreads_count(dmask != 0u) >= kTileDots;
+    if (many) {
+      double acc[4];
+      tile_dots<RM, CN>(pr, r0, cb, lr, lc, tA, tB, acc);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if ((dmask >> e) & 1u) cp[e] = from_dot(alpha, beta, acc[e], beta != 0.0 ? cp[e] : 0.0);
+    }
+  }
+  if (!many && dmask) {
+    for (int e = 0; e < ne; ++e)
+      if ((dmask >> e) & 1u) cp[e] = from_dot(alpha, beta, fp64_dot(pr, i0 + e, j), beta != 0.0 ? cp[e] : 0.0);
   }
   // counters: wave reduce, block reduce, one atomic per counter per block (exact integer sums)
   unsigned long long cu = cn.uncert, cr = cn.repair, cf = cn.safety;
