@@ -66,6 +66,9 @@ struct Cfg {
   static constexpr int DA = PA / NW, DB = PB / NW;     // per wave
   static constexpr int VM = DA + DB;                   // DMA instructions per wave and stage
   static constexpr int SMEM = NST * STAGE;
+  // k loop with the stage barrier between the two halves of a stage's MFMAs (below): pays with
+  // four waves per SIMD (the 16-wave kernel), not with the general kernel's two
+  static constexpr bool kSplit = NW >= 16;
   static_assert(PA % NW == 0 && PB % NW == 0 && FM >= 1 && FN >= 1, "tile split");
 };
 // general kernel: 256 threads, two workgroups per compute unit (72 KB of LDS each)
@@ -266,39 +269,100 @@ __device__ __forceinline__ void run_tile(uint8_t* lds, const i8_problem& P, cons
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = v4i{a0, a0, a0, a0};
 
-#pragma unroll
-  for (int q = 0; q < NST - 1; ++q)
-    if (q < nk) load(q, lds + q * C::STAGE);
-  int buf = 0;
-  if (nk <= 0) return;      // never scheduled: problems with kp == 0 get no tiles
-  __builtin_assume(nk > 0);  // one path into the epilogue (no zero-trip copy of the accumulators)
-  for (int kt = 0; kt < nk; ++kt) {
-    // stage kt landed (the NST - 2 stages after it may still be in flight; near the end fewer
-    // were issued, so wait for everything) and every wave is done with stage kt - 1
-    if (kt + NST - 2 < nk) wait_barrier<(NST - 2) * C::VM>(); else wait_barrier<0>();
-    if (kt + NST - 1 < nk) {
-      int b2 = buf + NST - 1;   // the ring slot of stage kt - 1
-      if (b2 >= NST) b2 -= NST;
-      load(kt + NST - 1, lds + b2 * C::STAGE);
+  // a final half stage (k in [kp, kp + 32)): zero A's chunks 2, 3 (B's duplicate chunk 0)
+  auto zero_half = [&](uint8_t* st) {
+    for (int c = tid; c < C::BM * 2; c += C::NT) {
+      const int row = c >> 1, ch = 2 + (c & 1);
+      *reinterpret_cast<uint4*>(st + row * kBK + swz(row, ch) * 16) = make_uint4(0u, 0u, 0u, 0u);
     }
-    uint8_t* st = lds + buf * C::STAGE;
-    if (kt == nk - 1 && (kp & 63)) {   // k in [kp, kp + 32): zero A's chunks 2, 3
-      for (int c = tid; c < C::BM * 2; c += C::NT) {
-        const int row = c >> 1, ch = 2 + (c & 1);
-        *reinterpret_cast<uint4*>(st + row * kBK + swz(row, ch) * 16) = make_uint4(0u, 0u, 0u, 0u);
-      }
-      wait_barrier<0>();
-    }
-    const uint32_t so = (uint32_t)(buf * C::STAGE);
-    v4i a[FM], b[FN];
-    read_frags<FN, C::SA>(b, b_addr + so);
-    read_frags<FM, 0>(a, a_addr + so);
-    lds_wait_frags<FM, FN>(a, b);   // the fragments are valid after this wait
+  };
+  auto mfmas = [&](const v4i* a, const v4i (&b)[FN], int i0, int i1) {
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+    for (int i = i0; i < i1; ++i)
 #pragma unroll
       for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], b[j], acc[i][j], 0, 0, 0);
-    buf = buf + 1 == NST ? 0 : buf + 1;
+  };
+  if constexpr (C::kSplit) {
+    // Stage s in ring slot s mod NST.  Iteration kt holds stage kt's fragments in registers: it
+    // issues the MFMAs of the first half of the A blocks, then (those queued on the matrix core)
+    // waits for stage kt + 1 and passes the barrier, refills slot kt (every wave holds its
+    // fragments) with stage kt + NST, reads stage kt + 1's first-half A fragments into the
+    // registers just consumed, issues the second half and reads the rest of stage kt + 1.  The
+    // barrier and the LDS latency overlap queued MFMA work (16-wave kernel: 2.4 % at k = 16384).
+    constexpr int H = FM / 2;
+#pragma unroll
+    for (int q = 0; q < NST; ++q)
+      if (q < nk) load(q, lds + q * C::STAGE);
+    if (nk <= 0) return;      // never scheduled: problems with kp == 0 get no tiles
+    __builtin_assume(nk > 0);  // one path into the epilogue (no zero-trip copy of the accumulators)
+    // stage 0 landed (stages 1 .. NST - 1 may still be in flight)
+    if (NST - 1 < nk) wait_barrier<(NST - 1) * C::VM>(); else wait_barrier<0>();
+    if (nk == 1 && (kp & 63)) {
+      zero_half(lds);
+      wait_barrier<0>();
+    }
+    v4i a[FM], b[FN];
+    read_frags<FN, C::SA>(b, b_addr);
+    read_frags<FM, 0>(a, a_addr);
+    int buf = 0;
+    for (int kt = 0; kt < nk; ++kt) {
+      lds_wait_frags<FM, FN>(a, b);   // stage kt's fragments are valid after this wait
+      mfmas(a, b, 0, H);
+      const bool more = kt + 1 < nk;
+      const int nb = buf + 1 == NST ? 0 : buf + 1;
+      const uint32_t so = (uint32_t)(nb * C::STAGE);
+      if (more) {
+        // stage kt + 1 landed (the NST - 2 stages after it may still be in flight; near the end
+        // fewer were issued, so wait for everything)
+        if (kt + NST - 1 < nk) wait_barrier<(NST - 2) * C::VM>(); else wait_barrier<0>();
+        if (kt + NST < nk) load(kt + NST, lds + buf * C::STAGE);
+        if (kt + 2 == nk && (kp & 63)) {
+          zero_half(lds + nb * C::STAGE);
+          wait_barrier<0>();
+        }
+        read_frags<H, 0>(a, a_addr + so);
+      }
+      mfmas(a, b, H, FM);
+      if (more) {
+        read_frags<FM - H, H * 1024>(a + H, a_addr + so);
+        read_frags<FN, C::SA>(b, b_addr + so);
+      }
+      buf = nb;
+    }
+    // the last iteration issues no reads: an explicit wait keeps every path into the epilogue
+    // free of pending LDS loads (also for the assembly dataflow check)
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  } else {
+    // Stage kt waits, passes the barrier (every wave is done with stage kt - 1), refills slot
+    // kt - 1 with stage kt + NST - 1, reads all its fragments and issues every MFMA.  With two
+    // workgroups per compute unit the other workgroup's MFMAs cover this one's waits.
+#pragma unroll
+    for (int q = 0; q < NST - 1; ++q)
+      if (q < nk) load(q, lds + q * C::STAGE);
+    int buf = 0;
+    if (nk <= 0) return;      // never scheduled: problems with kp == 0 get no tiles
+    __builtin_assume(nk > 0);  // one path into the epilogue (no zero-trip copy of the accumulators)
+    for (int kt = 0; kt < nk; ++kt) {
+      // stage kt landed (the NST - 2 stages after it may still be in flight; near the end fewer
+      // were issued, so wait for everything) and every wave is done with stage kt - 1
+      if (kt + NST - 2 < nk) wait_barrier<(NST - 2) * C::VM>(); else wait_barrier<0>();
+      if (kt + NST - 1 < nk) {
+        int b2 = buf + NST - 1;   // the ring slot of stage kt - 1
+        if (b2 >= NST) b2 -= NST;
+        load(kt + NST - 1, lds + b2 * C::STAGE);
+      }
+      if (kt == nk - 1 && (kp & 63)) {
+        zero_half(lds + buf * C::STAGE);
+        wait_barrier<0>();
+      }
+      const uint32_t so = (uint32_t)(buf * C::STAGE);
+      v4i a[FM], b[FN];
+      read_frags<FN, C::SA>(b, b_addr + so);
+      read_frags<FM, 0>(a, a_addr + so);
+      lds_wait_frags<FM, FN>(a, b);   // the fragments are valid after this wait
+      mfmas(a, b, 0, FM);
+      buf = buf + 1 == NST ? 0 : buf + 1;
+    }
   }
 
   // D block layout: lane l, register r -> row 4 (l / 16) + r, column l % 16; a lane's 4 values
