@@ -11,11 +11,12 @@
 //     consecutive table tiles, so one XCD works through contiguous runs of the table;
 //   * inside an entry tiles are rastered in groups of 8 tile-rows, m fastest, so the compute
 //     units of an XCD share A and B panels in L2.
-// Workgroups of 256 threads = 4 waves in a 2 x 2 arrangement, two workgroups per compute unit
-// (one's epilogue and barrier waits overlap the other's MFMA work):
-//   cfg 0: 256 x 128 tile, wave tile 128 x 64 = 8 x 4 blocks of v_mfma_i32_16x16x64_i8
-//   cfg 1: 128 x 128 tile, wave tile  64 x 64 = 4 x 4 blocks
-//   cfg 2:  64 x  64 tile, wave tile  32 x 32 = 2 x 2 blocks
+// General kernel: workgroups of 512 threads = 8 waves in a 4 x 2 arrangement, two workgroups per
+// compute unit (one's epilogue and barrier waits overlap the other's MFMA work):
+//   cfg 0: 256 x 128 tile, wave tile 64 x 64 = 4 x 4 blocks of v_mfma_i32_16x16x64_i8
+//   cfg 1: 128 x 128 tile, wave tile 32 x 64 = 2 x 4 blocks
+//   cfg 2:  64 x  64 tile, wave tile 16 x 32 = 1 x 2 blocks
+// Large-tile kernel: one workgroup of 16 waves (4 x 4) per compute unit, 256 x 256 tiles.
 // K advances in stages of 64.  Operands go HBM -> LDS directly (global_load_lds_dwordx4, no VGPR
 // round trip) into a ring of 3 LDS stages, two stages ahead of the MFMA work; one barrier per
 // stage.  An LDS row holds the 64 k-bytes of one A / B row as 4 chunks of 16 bytes, chunk index
@@ -63,19 +64,22 @@ struct Cfg {
   static constexpr int FM = WM / 16, FN = WN / 16;     // 16 x 16 MFMA blocks per wave
   static constexpr int SA = BM * kBK, SB = BN * kBK, STAGE = SA + SB;
   static constexpr int PA = SA / 1024, PB = SB / 1024; // 1 KB DMA pieces per operand and stage
-  static constexpr int DA = PA / NW, DB = PB / NW;     // per wave
-  static constexpr int VM = DA + DB;                   // DMA instructions per wave and stage
+  // a stage's A pieces then B pieces, dealt to the waves round-robin: piece g = wave + NW q
+  static constexpr int VM = (PA + PB) / NW;            // DMA instructions per wave and stage
   static constexpr int SMEM = NST * STAGE;
-  // k loop with the stage barrier between the two halves of a stage's MFMAs (below): pays with
-  // four waves per SIMD (the 16-wave kernel), not with the general kernel's two
+  // k loop with the stage barrier between the two halves of a stage's MFMAs (below): pays for
+  // the 16-wave kernel (one workgroup per compute unit), not for the general kernel's two
+  // workgroups
   static constexpr bool kSplit = NW >= 16;
-  static_assert(PA % NW == 0 && PB % NW == 0 && FM >= 1 && FN >= 1, "tile split");
+  static_assert((PA + PB) % NW == 0 && FM >= 1 && FN >= 1, "tile split");
 };
-// general kernel: 256 threads, two workgroups per compute unit (72 KB of LDS each)
-using Cfg0 = Cfg<256, 128, 2, 2, 3>;
-using Cfg1 = Cfg<128, 128, 2, 2, 3>;
-using Cfg2 = Cfg<64, 64, 2, 2, 3>;
-constexpr int kThreads = 256;
+// general kernel: 512 threads = 8 waves of (BM / 4) x (BN / 2), two workgroups per compute unit
+// (72 KB of LDS each, four waves per SIMD); against 4 waves of (BM / 2) x (BN / 2) the 256 x 128
+// tiles of 1024^3 products run 1.4-3 % faster (more waves hide the DMA and LDS waits)
+using Cfg0 = Cfg<256, 128, 4, 2, 3>;
+using Cfg1 = Cfg<128, 128, 4, 2, 3>;
+using Cfg2 = Cfg<64, 64, 4, 2, 3>;
+constexpr int kThreads = 512;
 constexpr int kSmem = Cfg0::SMEM;
 static_assert(Cfg1::SMEM <= kSmem && Cfg2::SMEM <= kSmem, "smem");
 // large-tile kernel: 1024 threads = 16 waves of 64 x 64 (4 per SIMD, so one wave's LDS reads and
@@ -110,16 +114,14 @@ __device__ __forceinline__ void wait_barrier() {
 // compiler-generated copy of a fragment can be placed before its data has arrived.
 template <int FM, int FN>
 __device__ __forceinline__ void lds_wait_frags(v4i (&a)[FM], v4i (&b)[FN]) {
-  if constexpr (FM == 8 && FN == 4) {
-    asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]), "+v"(a[6]), "+v"(a[7]),
-                   "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]));
-  } else if constexpr (FM == 4 && FN == 4) {
+  if constexpr (FM == 4 && FN == 4) {
     asm volatile("s_waitcnt lgkmcnt(0)"
                  : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]));
+  } else if constexpr (FM == 2 && FN == 4) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a[0]), "+v"(a[1]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]));
   } else {
-    static_assert(FM == 2 && FN == 2, "fragment counts");
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a[0]), "+v"(a[1]), "+v"(b[0]), "+v"(b[1]));
+    static_assert(FM == 1 && FN == 2, "fragment counts");
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a[0]), "+v"(b[0]), "+v"(b[1]));
   }
 }
 
@@ -138,26 +140,36 @@ __device__ __forceinline__ StageSrc stage_src(const int8_t* plane, int rows, int
   return StageSrc{plane + (size_t)row0 * kp + k0, kp, kp - k0};
 }
 
+// This wave's DMA pieces of a stage (wave-uniform): fa(A piece) and fb(B piece), C::VM in all.
+template <class C, class FA, class FB>
+__device__ __forceinline__ void for_pieces(int wave, FA&& fa, FB&& fb) {
+  if constexpr (C::PA % C::NW == 0) {   // the A / B split is a multiple of the wave count
+#pragma unroll
+    for (int q = 0; q < C::PA / C::NW; ++q) fa(wave + C::NW * q);
+#pragma unroll
+    for (int q = 0; q < C::PB / C::NW; ++q) fb(wave + C::NW * q);
+  } else {
+#pragma unroll
+    for (int q = 0; q < C::VM; ++q) {
+      const int g = wave + C::NW * q;
+      if (g < C::PA) fa(g); else fb(g - C::PA);
+    }
+  }
+}
+
 template <class C>
 __device__ __forceinline__ void dma_stage(const StageSrc& a, const StageSrc& b, int m_rem, int n_rem, uint8_t* st,
                                           int wave, int lane) {
   const int r_in = lane >> 2, pc = lane & 3;
-#pragma unroll
-  for (int q = 0; q < C::DA; ++q) {
-    const int piece = wave + C::NW * q, row = piece * 16 + r_in;
+  auto piece_of = [&](const StageSrc& o, int rem, int piece, uint8_t* dst) {
+    const int row = piece * 16 + r_in;
     const int kk = 16 * swz(row, pc);
-    const int rr = row < m_rem ? row : m_rem - 1;
-    __builtin_amdgcn_global_load_lds((const void*)(a.base + (size_t)rr * a.stride + (kk < a.lim ? kk : 0)),
-                                     GGEMM_LDS(st + piece * 1024), 16, 0, 0);
-  }
-#pragma unroll
-  for (int q = 0; q < C::DB; ++q) {
-    const int piece = wave + C::NW * q, row = piece * 16 + r_in;
-    const int kk = 16 * swz(row, pc);
-    const int rr = row < n_rem ? row : n_rem - 1;
-    __builtin_amdgcn_global_load_lds((const void*)(b.base + (size_t)rr * b.stride + (kk < b.lim ? kk : 0)),
-                                     GGEMM_LDS(st + C::SA + piece * 1024), 16, 0, 0);
-  }
+    const int rr = row < rem ? row : rem - 1;
+    __builtin_amdgcn_global_load_lds((const void*)(o.base + (size_t)rr * o.stride + (kk < o.lim ? kk : 0)),
+                                     GGEMM_LDS(dst + piece * 1024), 16, 0, 0);
+  };
+  for_pieces<C>(wave, [&](int piece) { piece_of(a, m_rem, piece, st); },
+                [&](int piece) { piece_of(b, n_rem, piece, st + C::SA); });
 }
 
 // The same stage when every row of the tile exists and every chunk is inside the row (the common
@@ -167,18 +179,16 @@ __device__ __forceinline__ void dma_stage(const StageSrc& a, const StageSrc& b, 
 template <class C>
 __device__ __forceinline__ void dma_stage_full(const int8_t* a, const int8_t* b, int a_stride, int b_stride,
                                                uint32_t a_lane, uint32_t b_lane, uint8_t* st, int wave) {
-#pragma unroll
-  for (int q = 0; q < C::DA; ++q) {
-    const int piece = wave + C::NW * q;
-    __builtin_amdgcn_global_load_lds((const void*)(a + (size_t)piece * 16 * a_stride + a_lane),
-                                     GGEMM_LDS(st + piece * 1024), 16, 0, 0);
-  }
-#pragma unroll
-  for (int q = 0; q < C::DB; ++q) {
-    const int piece = wave + C::NW * q;
-    __builtin_amdgcn_global_load_lds((const void*)(b + (size_t)piece * 16 * b_stride + b_lane),
-                                     GGEMM_LDS(st + C::SA + piece * 1024), 16, 0, 0);
-  }
+  for_pieces<C>(
+      wave,
+      [&](int piece) {
+        __builtin_amdgcn_global_load_lds((const void*)(a + (size_t)piece * 16 * a_stride + a_lane),
+                                         GGEMM_LDS(st + piece * 1024), 16, 0, 0);
+      },
+      [&](int piece) {
+        __builtin_amdgcn_global_load_lds((const void*)(b + (size_t)piece * 16 * b_stride + b_lane),
+                                         GGEMM_LDS(st + C::SA + piece * 1024), 16, 0, 0);
+      });
 }
 
 // C mod p in [0, p) from u = C + bias >= 0: q = umulhi(u, mc) with mc = ceil(2^32 / p) is floor(u / p)
