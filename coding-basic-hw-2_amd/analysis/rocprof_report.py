@@ -31,6 +31,8 @@ Usage
 """
 import argparse
 import csv
+import json
+import os
 import re
 import statistics
 import sys
@@ -165,8 +167,9 @@ def copy_factor(path, counter, true_kib):
     return max(vals) / true_kib
 
 
-def traffic(args):
-    """{kernel: (read_bytes, write_bytes)} per dispatch, or {} without counter files."""
+def traffic_detail(args):
+    """{kernel: record} per dispatch: mean FETCH_SIZE / WRITE_SIZE (KiB), the copy factors and the
+    calibrated read / write bytes; {} without counter files."""
     if not (args.fetch and args.write):
         return {}
     kib = args.copy_bytes / 1024.0
@@ -177,8 +180,37 @@ def traffic(args):
     for k in fe:
         if stage_of(k) in (None, "memops") or k not in wr:
             continue
-        out[k] = (statistics.fmean(fe[k]) / ff * 1024.0, statistics.fmean(wr[k]) / fw * 1024.0)
+        f_kib, w_kib = statistics.fmean(fe[k]), statistics.fmean(wr[k])
+        out[k] = {"fetch_kib": f_kib, "write_kib": w_kib, "fetch_factor": ff, "write_factor": fw,
+                  "read_bytes": f_kib / ff * 1024.0, "write_bytes": w_kib / fw * 1024.0}
     return out
+
+
+def traffic(args):
+    """{kernel: (read_bytes, write_bytes)} per dispatch, or {} without counter files."""
+    return {k: (r["read_bytes"], r["write_bytes"]) for k, r in traffic_detail(args).items()}
+
+
+def write_traffic_json(args, kt):
+    """Record the INT8 GEMM's HBM bytes per launch under args.traffic_key in args.traffic_json (the
+    figure bench.py reports as roofline.traffic); other keys of an existing file are kept."""
+    det = traffic_detail(args)
+    gemm = [k for k in det if stage_of(k) == "i8_gemm"]
+    if not gemm:
+        raise SystemExit("--traffic-json: no INT8 GEMM kernel with FETCH_SIZE and WRITE_SIZE counters")
+    k = max(gemm, key=lambda g: kt[g][1] * kt[g][2] if g in kt else 0.0)   # most busy time
+    r = det[k]
+    rec = {"kernel": k, "fetch_kib": r["fetch_kib"], "write_kib": r["write_kib"], "fetch_factor": r["fetch_factor"],
+           "write_factor": r["write_factor"], "traffic_bytes": int(round(r["read_bytes"] + r["write_bytes"]))}
+    data = {}
+    if os.path.exists(args.traffic_json):
+        with open(args.traffic_json) as f:
+            data = json.load(f)
+    data[args.traffic_key] = rec
+    with open(args.traffic_json, "w") as f:
+        json.dump(data, f, indent=1)
+        f.write("\n")
+    return rec
 
 
 def fmt(x, nd=1):
@@ -229,6 +261,8 @@ def report(args):
             f.write(text)
     else:
         sys.stdout.write(text)
+    if getattr(args, "traffic_json", None):
+        write_traffic_json(args, kt)
     if args.csv:
         with open(args.csv, "w", newline="") as f:
             w = csv.DictWriter(f, fieldnames=list(rows[0].keys()) if rows else ["kernel"])
@@ -248,6 +282,8 @@ def main(argv=None):
     ap.add_argument("--copy-bytes", type=float, default=float(1 << 30), help="bytes read (= written) per copy")
     ap.add_argument("-o", "--out", help="markdown output (default stdout)")
     ap.add_argument("--csv", help="per-kernel CSV output")
+    ap.add_argument("--traffic-json", help="record the INT8 GEMM's HBM bytes per launch in this JSON file")
+    ap.add_argument("--traffic-key", default="uniform", help="workload key of that record")
     report(ap.parse_args(argv))
 
 

@@ -102,3 +102,27 @@ def test_roofline_and_traffic(tmp_path):
     assert by["prep_kernel"]["hbm_read_gb"] == pytest.approx(100 * 1024 / 1e9)
     text = (tmp_path / "r.md").read_text()
     assert "Calls (median over 5)" in text
+
+
+def test_traffic_json_record(tmp_path):
+    """--traffic-json writes the INT8 GEMM's calibrated bytes per launch (the figure bench.py
+    reports as roofline.traffic) under its key and keeps the other keys of the file."""
+    rr = _tool()
+    tr = tmp_path / "t.csv"
+    _trace(tr, TIMELINE)
+    fe, wr, cf, cw = (tmp_path / f for f in ("fe.csv", "wr.csv", "cf.csv", "cw.csv"))
+    _counters(fe, "FETCH_SIZE", [(I8, 100.0), (I8, 300.0), (PREP, 50.0)])
+    _counters(wr, "WRITE_SIZE", [(I8, 64.0), (PREP, 32.0)])
+    _counters(cf, "FETCH_SIZE", [(COPY, 524288.0)])
+    _counters(cw, "WRITE_SIZE", [(COPY, 1048576.0)])
+    js = tmp_path / "hbm.json"
+    js.write_text('{"large": {"traffic_bytes": 7}}')
+    rr.main([str(tr), "--fetch", str(fe), "--write", str(wr), "--copy-fetch", str(cf), "--copy-write", str(cw),
+             "-o", str(tmp_path / "r.md"), "--traffic-json", str(js), "--traffic-key", "uniform"])
+    data = rr.json.loads(js.read_text())
+    assert data["large"] == {"traffic_bytes": 7}
+    rec = data["uniform"]
+    assert rec["kernel"] == "i8_large_kernel"
+    assert rec["fetch_kib"] == pytest.approx(200.0) and rec["write_kib"] == pytest.approx(64.0)
+    assert rec["fetch_factor"] == pytest.approx(0.5) and rec["write_factor"] == pytest.approx(1.0)
+    assert rec["traffic_bytes"] == round((400 + 64) * 1024)
