@@ -22,7 +22,10 @@
 //     park the doubles in LDS k-major; then every thread takes 16 consecutive k of one row,
 //     computes the residues and writes each plane with one 128-bit store.
 //   * B (column-major = K contiguous): 32 lanes per column, 4 consecutive k per lane: 1 KB
-//     coalesced loads, 128 contiguous residue bytes per plane per store.
+//     coalesced loads, 128 contiguous residue bytes per plane per store.  With two-word digits and
+//     k <= 1024 a column is read once: lane l keeps k = l (mod 32) in registers (its norm chain)
+//     and receives each chunk's 4 consecutive k through a 1 KB LDS exchange row of its column.
+//     The kernel is bounded to 128 VGPRs (four workgroups per compute unit).
 // Floating-point contraction is off in this file: the only fused operations are the explicit
 // fma() calls, which are the reference's own.
 #include <cmath>
@@ -356,6 +359,8 @@ __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ t
 }
 
 // ---------------------------------------------------------------------------- B columns
+constexpr int kBReg = 32;   // column values per lane held in registers (K <= 32 kBReg: one read of B)
+
 template <bool kWide>
 __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ tab, int blk, int split,
                           int nsplit, PrepShared& sm, unsigned long long* cnt, bool packed) {
@@ -366,22 +371,38 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
   const double* __restrict__ b = pr.B + (size_t)j * pr.ldb;
   const double T = tab->T[N];
 
+  // K <= 32 kBReg: the column is read once; lane l keeps k = l + 32 t in registers (its norm chain,
+  // zeros past K change neither the max nor the sums) and gets the residue pass's 4 consecutive k
+  // per chunk through a wave-private LDS exchange row
+  // (two-word digits only: with three-word digits the kernel would exceed 128 VGPRs)
+  const bool single = !kWide && K <= 32 * kBReg;
+  double v[kBReg];
   double mx = 0.0, ss = 0.0;
-  int k = lane;
-  for (; k + 32 * 7 < K; k += 32 * 8) {   // 8 loads in flight, then the ordered chain
-    double a[8];
+  if (single) {
 #pragma unroll
-    for (int t = 0; t < 8; ++t) a[t] = b[k + 32 * t];
+    for (int t = 0; t < kBReg; ++t) v[t] = lane + 32 * t < K ? b[lane + 32 * t] : 0.0;
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      mx = fmax(mx, fabs(a[t]));
-      ss = fma(a[t], a[t], ss);
+    for (int t = 0; t < kBReg; ++t) {
+      mx = fmax(mx, fabs(v[t]));
+      ss = fma(v[t], v[t], ss);
     }
-  }
-  for (; k < K; k += 32) {
-    const double a = b[k];
-    mx = fmax(mx, fabs(a));
-    ss = fma(a, a, ss);
+  } else {
+    int k = lane;
+    for (; k + 32 * 7 < K; k += 32 * 8) {   // 8 loads in flight, then the ordered chain
+      double a[8];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) a[t] = b[k + 32 * t];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        mx = fmax(mx, fabs(a[t]));
+        ss = fma(a[t], a[t], ss);
+      }
+    }
+    for (; k < K; k += 32) {
+      const double a = b[k];
+      mx = fmax(mx, fabs(a));
+      ss = fma(a, a, ss);
+    }
   }
 #pragma unroll
   for (int o = 16; o; o >>= 1) mx = fmax(mx, __shfl_xor(mx, o, 32));
@@ -389,9 +410,17 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
   if (resc) {
     const int e = -ilogb(mx);
     ss = 0.0;
-    for (int k = lane; k < K; k += 32) {
-      const double a = mul_pow2(b[k], e);
-      ss = fma(a, a, ss);
+    if (single) {
+#pragma unroll
+      for (int t = 0; t < kBReg; ++t) {
+        const double a = mul_pow2(v[t], e);
+        ss = fma(a, a, ss);
+      }
+    } else {
+      for (int k = lane; k < K; k += 32) {
+        const double a = mul_pow2(b[k], e);
+        ss = fma(a, a, ss);
+      }
     }
   }
 #pragma unroll
@@ -412,18 +441,16 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
   const int c0 = min(nchunk, split * per), c1 = min(nchunk, c0 + per);
   // split 0 walks every chunk (ordered sums) but writes residues only for its own range; lane L
   // owns k = 128 ch + 4 L + e
-  for (int ch = (split == 0 ? 0 : c0); ch < (split == 0 ? nchunk : c1); ++ch) {
+  // chunk ch's residues from its values a (lane l: k = 128 ch + 4 l + e)
+  auto chunk = [&](int ch, const double (&a)[4]) {
     const int k0 = 128 * ch + 4 * lane;
-    if (k0 >= Kp) continue;
+    if (k0 >= Kp) return;
     int8_t* const base = B8 + (packed ? packed_offset(j, k0, n, Kp) : (size_t)j * Kp + k0);
-    double a[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) a[e] = (k0 + e < K) ? b[k0 + e] : 0.0;
     const bool write = ch >= c0 && ch < c1;
     if (nf) {
       if (write)
         for (int l = 0; l <= N; ++l) *reinterpret_cast<uint32_t*>(base + (size_t)l * pr.b8_mod_stride) = 0u;
-      continue;
+      return;
     }
     double xs[4], xt[4];
     scaled<4>(a, sh, xs);
@@ -436,12 +463,42 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
         na2 = fma(xt[e], xt[e], na2);
       }
     }
-    if (!write) continue;
+    if (!write) return;
     planes<4, kWide>(xt, N, tab, 0, base, pr.b8_mod_stride);
     uint32_t q = 0u;
 #pragma unroll
     for (int e = 0; e < 4; ++e) q |= abs_u8(a[e], sg) << (8 * e);
     *reinterpret_cast<uint32_t*>(base + (size_t)N * pr.b8_mod_stride) = q;
+  };
+  const int ch0 = split == 0 ? 0 : c0, ch1 = split == 0 ? nchunk : c1;   // chunks walked here
+  if (single) {
+    // lane l holds k = 128 ch + 32 jj + l (jj < 4) of chunk ch in v[4 ch + jj]: through this column's
+    // LDS exchange row to k = 128 ch + 4 l + e; unrolled so that the register indices are static
+    double* const xb = reinterpret_cast<double*>(&sm.tile[0][0]) + 128 * w;
+#pragma unroll
+    for (int ch = 0; ch < kBReg / 4; ++ch) {
+      if (ch < ch0 || ch >= ch1) continue;   // column-uniform
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) xb[32 * jj + lane] = v[4 * ch + jj];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      double a[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) a[e] = xb[4 * lane + e];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");   // the reads precede the next chunk's writes
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      chunk(ch, a);
+    }
+  } else {
+    for (int ch = ch0; ch < ch1; ++ch) {
+      const int k0 = 128 * ch + 4 * lane;
+      double a[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) a[e] = (k0 + e < K) ? b[k0 + e] : 0.0;
+      chunk(ch, a);
+    }
   }
   if (split != 0) return;
 #pragma unroll
@@ -458,7 +515,7 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
 // kWide: three-word digits (any N); the two-word kernel is launched only for calls whose every
 // problem has T_N < 1.5 2^62
 template <bool kWide>
-__global__ void __launch_bounds__(kThreads) prep_kernel(const oz2_problem* __restrict__ probs, int a_blocks,
+__global__ void __launch_bounds__(kThreads, 4) prep_kernel(const oz2_problem* __restrict__ probs, int a_blocks,
                                                         const CrtTables* __restrict__ tab,
                                                         unsigned long long* __restrict__ cnt, int fold_q,
                                                         int packed) {

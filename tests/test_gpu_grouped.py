@@ -178,6 +178,32 @@ def test_fixed_moduli_digit_widths(path, N):
     check_case(case, path, cfg, st, O.REPAIR_COUNT)
 
 
+@pytest.mark.parametrize("N", [12, 16])
+def test_single_read_columns_special_values(N):
+    """With two-word digits (N <= 16) the production prep reads a B column with k <= 1024 once and
+    keeps it in registers: k at and around the chunk (128) and register (1024) limits (1025 takes
+    the two-pass path), the rescale path (2^650 and 2^-700 magnitudes, one 1e300 entry), a zero
+    column and NaN / Inf columns, all in one call; bitwise against the oracle with equal counters."""
+    shapes = [(40, 24, 1), (40, 24, 33), (36, 20, 127), (33, 17, 129), (48, 40, 1000), (40, 24, 1024),
+              (40, 24, 1025)]
+    case = Case(shapes, 20261220 + N, phi=1.0, beta=0.5)
+    case.hp[2].B[:] = np.ldexp(case.hp[2].B, 650)
+    case.hp[3].B[:] = np.ldexp(case.hp[3].B, -700)
+    h = case.hp[4]
+    h.B[3 * h.ldb: 3 * h.ldb + h.k] = 0.0
+    h.B[5 + 7 * h.ldb] = np.nan
+    h.B[999 + 11 * h.ldb] = np.inf
+    h = case.hp[5]
+    h.B[1023 + 2 * h.ldb] = 1e300
+    case.alloc()
+    cfg = G.Config(N, 1e-15, 0, 0)
+    say(f"single-read columns N={N}")
+    rc, st = run(case, G.PATH_EMU_GROUPED, cfg)
+    assert rc == 0
+    assert st.moduli_min == st.moduli_max == N
+    check_case(case, G.PATH_EMU_GROUPED, cfg, st, O.REPAIR_COUNT)
+
+
 @pytest.mark.parametrize("path", [G.PATH_EMU_GROUPED, G.PATH_AUTO, G.PATH_EMU_LOOP, G.PATH_EMU_LOOP_BATCHED])
 def test_uniform_group_beta(path):
     """Config-2 shape family, reduced: G=8 x 192^3, (U-0.5)exp(0.5 Z), alpha=1, beta=0.5."""
