@@ -7,12 +7,13 @@
 // longest-processing-time order (heaviest tiles first, the reference's scheduling contract,
 // src/int8_grouped_gemm.cu:602-675).  Workgroup b takes one tile:
 //   * XCD-aware dispatch: MI355X deals workgroups round-robin to its 8 XCDs (b mod 8), each with
-//     its own L2.  Workgroup b is mapped to tile chunk (b mod 8) + 8 (b / (8 C)) of C = 16
-//     consecutive table tiles, so one XCD works through contiguous runs of the table;
-//   * inside an entry tiles are rastered in groups of 4 tile-rows, m fastest, so the compute
-//     units of an XCD share A and B panels in L2 (chunks of 16 and groups of 4 against 32 and 8:
-//     about 1 % faster on 8192^2 x 16384 and on 1024^3 products over two boxes, within the
-//     box-to-box spread; groups of 16 tile-rows 10 % slower, chunks of 64 1 % slower).
+//     its own L2.  Workgroup b is mapped to tile chunk (b mod 8) + 8 (b / (8 C)) of C = 32
+//     consecutive table tiles, so one XCD works through contiguous runs of the table (a 1024^2
+//     product's 32 tiles share one L2: each plane is read from HBM once; chunks of 16 read
+//     the planes of 1024^3 products 1.5 times, at equal speed);
+//   * inside an entry tiles are rastered in groups of 8 tile-rows, m fastest, so the compute
+//     units of an XCD share A and B panels in L2 (16 tile-rows measured 10 % slower at
+//     8192^2 x 16384).
 // General kernel: workgroups of 512 threads = 8 waves in a 4 x 2 arrangement, two workgroups per
 // compute unit (one's epilogue and barrier waits overlap the other's MFMA work):
 //   cfg 0: 256 x 128 tile, wave tile 64 x 64 = 4 x 4 blocks of v_mfma_i32_16x16x64_i8
@@ -53,9 +54,9 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kBK = 64;
-constexpr int kChunk = 16;   // tiles per XCD chunk
+constexpr int kChunk = 32;   // tiles per XCD chunk
 constexpr int kXcds = 8;
-constexpr int kGroupM = 4;   // tile-rows per raster group
+constexpr int kGroupM = 8;   // tile-rows per raster group
 
 // Tile BM x BN computed by WGM x WGN waves through an NST-stage LDS ring.
 template <int BM_, int BN_, int WGM_, int WGN_, int NST_>
