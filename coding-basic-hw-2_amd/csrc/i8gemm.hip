@@ -7,13 +7,14 @@
 // longest-processing-time order (heaviest tiles first, the reference's scheduling contract,
 // src/int8_grouped_gemm.cu:602-675).  Workgroup b takes one tile:
 //   * XCD-aware dispatch: MI355X deals workgroups round-robin to its 8 XCDs (b mod 8), each with
-//     its own L2.  Workgroup b is mapped to tile chunk (b mod 8) + 8 (b / (8 C)) of C = 32
-//     consecutive table tiles, so one XCD works through contiguous runs of the table (a 1024^2
-//     product's 32 tiles share one L2: each plane is read from HBM once; chunks of 16 read
-//     the planes of 1024^3 products 1.5 times, at equal speed);
-//   * inside an entry tiles are rastered in groups of 8 tile-rows, m fastest, so the compute
-//     units of an XCD share A and B panels in L2 (16 tile-rows measured 10 % slower at
-//     8192^2 x 16384).
+//     its own L2.  Workgroup b is mapped to tile chunk (b mod 8) + 8 (b / (8 C)) of C
+//     consecutive table tiles, so one XCD works through contiguous runs of the table;
+//   * inside an entry tiles are rastered in groups of G tile-rows, m fastest, so the compute
+//     units of an XCD share A and B panels in L2.
+//   General kernel C = 32, G = 8: a 1024^2 product's 32 tiles share one L2 and each plane is read
+//   from HBM once (C = 16 reads them 1.5 times at equal speed).  Large-tile kernel C = 16, G = 4:
+//   on 8192^2 x 16384 products 1-3 % faster than 32 / 8 in two of three same-box comparisons,
+//   equal in the third (G = 16: 10 % slower).
 // General kernel: workgroups of 512 threads = 8 waves in a 4 x 2 arrangement, two workgroups per
 // compute unit (one's epilogue and barrier waits overlap the other's MFMA work):
 //   cfg 0: 256 x 128 tile, wave tile 64 x 64 = 4 x 4 blocks of v_mfma_i32_16x16x64_i8
@@ -54,9 +55,10 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kBK = 64;
-constexpr int kChunk = 32;   // tiles per XCD chunk
+// XCD chunk (tiles) and raster group (tile-rows) of the two kernels
+constexpr int kChunk = 32, kGroupM = 8;     // general kernel
+constexpr int kChunkL = 16, kGroupML = 4;   // large-tile kernel
 constexpr int kXcds = 8;
-constexpr int kGroupM = 8;   // tile-rows per raster group
 
 // Tile BM x BN computed by WGM x WGN waves through an NST-stage LDS ring.
 template <int BM_, int BN_, int WGM_, int WGN_, int NST_>
@@ -431,16 +433,17 @@ __device__ __forceinline__ void run_tile(uint8_t* lds, const i8_problem& P, cons
 struct TileRef {
   int pi, cfg, local;
 };
+template <int CH>
 __device__ __forceinline__ TileRef find_tile(const int* __restrict__ sched) {
   const int total = sched[0];
   const int ne = sched[1];
   const int b = blockIdx.x;
-  const int span = kXcds * kChunk;
+  const int span = kXcds * CH;
   const int full = total / span * span;
   int tile = b;
   if (b < full) {
     const int x = b % kXcds, q = b / kXcds;
-    tile = (q / kChunk) * span + x * kChunk + (q % kChunk);
+    tile = (q / CH) * span + x * CH + (q % CH);
   }
   const int* prefix = sched + kSchedHdr;
   const int* entry = prefix + ne + 1;
@@ -459,12 +462,13 @@ __device__ __forceinline__ TileRef find_tile(const int* __restrict__ sched) {
   const int e = entry[lo];
   return TileRef{e >> 2, e & 3, tile - (per > 0 ? lo * per : prefix[lo])};
 }
-// grouped raster inside a product: blocks of kGroupM tile-rows, m fastest inside a block
+// grouped raster inside a product: blocks of GM tile-rows, m fastest inside a block
+template <int GM>
 __device__ __forceinline__ void raster(int local, int m, int n, int bm, int bn, int& tm, int& tn) {
   const int tiles_m = (m + bm - 1) / bm, tiles_n = (n + bn - 1) / bn;
-  const int per_group = kGroupM * tiles_n;   // blocks of kGroupM tile-rows, m fastest inside a block
-  const int g = local / per_group, first_m = g * kGroupM;
-  const int gsz = min(kGroupM, tiles_m - first_m);
+  const int per_group = GM * tiles_n;
+  const int g = local / per_group, first_m = g * GM;
+  const int gsz = min(GM, tiles_m - first_m);
   const int r = local - g * per_group;
   tm = first_m + r % gsz;
   tn = r / gsz;
@@ -474,12 +478,12 @@ __global__ void __launch_bounds__(kThreads, 2) i8_grouped_kernel(const i8_proble
                                                                  const I8Epi* __restrict__ epis,
                                                                  const int* __restrict__ sched) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
-  const TileRef t = find_tile(sched);
+  const TileRef t = find_tile<kChunk>(sched);
   const i8_problem P = probs[t.pi];
   I8Epi epi{0u, 1u, 0u, 0u};
   if (epis) epi = epis[t.pi];
   int tm, tn;
-  raster(t.local, P.m, P.n, i8_tile_m(t.cfg), i8_tile_n(t.cfg), tm, tn);
+  raster<kGroupM>(t.local, P.m, P.n, i8_tile_m(t.cfg), i8_tile_n(t.cfg), tm, tn);
   switch (t.cfg) {
     case 0: (epi.mode & kEpiPacked) ? run_tile<Cfg0, true>(lds, P, epi, tm, tn) : run_tile<Cfg0, false>(lds, P, epi, tm, tn); break;
     case 1: (epi.mode & kEpiPacked) ? run_tile<Cfg1, true>(lds, P, epi, tm, tn) : run_tile<Cfg1, false>(lds, P, epi, tm, tn); break;
@@ -492,12 +496,12 @@ __global__ void __launch_bounds__(kThreadsL, 1) i8_large_kernel(const i8_problem
                                                                 const I8Epi* __restrict__ epis,
                                                                 const int* __restrict__ sched) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
-  const TileRef t = find_tile(sched);
+  const TileRef t = find_tile<kChunkL>(sched);
   const i8_problem P = probs[t.pi];
   I8Epi epi{0u, 1u, 0u, 0u};
   if (epis) epi = epis[t.pi];
   int tm, tn;
-  raster(t.local, P.m, P.n, CfgL::BM, CfgL::BN, tm, tn);
+  raster<kGroupML>(t.local, P.m, P.n, CfgL::BM, CfgL::BN, tm, tn);
   if (epi.mode & kEpiPacked) run_tile<CfgL, true>(lds, P, epi, tm, tn);
   else run_tile<CfgL, false>(lds, P, epi, tm, tn);
 }
