@@ -375,7 +375,12 @@ __device__ __forceinline__ void run_tile(uint8_t* lds, const i8_problem& P, cons
       read_frags<FN, C::SA>(b, b_addr + so);
       read_frags<FM, 0>(a, a_addr + so);
       lds_wait_frags<FM, FN>(a, b);   // the fragments are valid after this wait
+      // raised wave priority while the stage's MFMAs issue, ahead of the other waves' DMA, LDS
+      // reads and epilogue (0.4-1.1 % faster on 1024^3 products in two same-box comparisons; the
+      // 16-wave kernel measured 1 % slower with it)
+      __builtin_amdgcn_s_setprio(1);
       mfmas(a, b, 0, FM);
+      __builtin_amdgcn_s_setprio(0);
       buf = buf + 1 == NST ? 0 : buf + 1;
     }
   }
