@@ -151,13 +151,27 @@ __device__ __forceinline__ void wave_dots(const oz2_problem& pr, int wr0, int wc
   const int sk = lane >> 2, sr = 4 * (lane & 3);   // staging: k-row sk, rows / k sr .. sr + 3
 #pragma unroll
   for (int e = 0; e < 4; ++e) acc[e] = 0.0;
+  if (K <= 0) return;
+  // the chunk's 8 values per lane come from clamped (always valid) addresses, all loads in flight
+  // at once (no prefetch across chunks: it would cost the kernel its fifth wave per SIMD); values
+  // outside the problem stage as zero
+  const int colB = min(wc0 + sk, n - 1);
+  const bool inB = wc0 + sk < n;
+  double va[4], vb[4];
+  auto fetch = [&](int kc) {
+    const size_t ka = (size_t)min(kc + sk, K - 1) * lda;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) va[e] = A[(size_t)min(wr0 + sr + e, m - 1) + ka];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) vb[e] = B[(size_t)min(kc + sr + e, K - 1) + (size_t)colB * ldb];
+  };
   for (int kc = 0; kc < K; kc += kKC) {
     const int kn = min(kKC, K - kc);
+    fetch(kc);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {   // A: wA[kk][r] (16 x 16), B: wB[col][kk] (16 x 17)
-      const int r = wr0 + sr + e, kb = kc + sr + e;
-      wA[sk * 16 + sr + e] = (r < m && sk < kn) ? A[(size_t)r + (size_t)(kc + sk) * lda] : 0.0;
-      wB[sk * (kKC + 1) + sr + e] = (wc0 + sk < n && sr + e < kn) ? B[(size_t)kb + (size_t)(wc0 + sk) * ldb] : 0.0;
+      wA[sk * 16 + sr + e] = (wr0 + sr + e < m && sk < kn) ? va[e] : 0.0;
+      wB[sk * (kKC + 1) + sr + e] = (inB && sr + e < kn) ? vb[e] : 0.0;
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -187,18 +201,34 @@ __device__ __forceinline__ void tile_dots(const oz2_problem& pr, int r0, int cb,
   const int m = pr.m, n = pr.n, K = pr.k;
 #pragma unroll
   for (int e = 0; e < 4; ++e) acc[e] = 0.0;
+  if (K <= 0) return;   // workgroup-uniform
+  // a thread's staging elements: A x = tid + kThreads i (kk = x / RM, r = x % RM), B x = tid when
+  // below CN kKC; loaded from clamped (always valid) addresses, all of a chunk in flight at once
+  // (no prefetch across chunks: it would take this kernel past 102 VGPRs); values outside the
+  // problem stage as zero
+  constexpr int NA = kKC * RM / kThreads;
+  static_assert(kKC * RM % kThreads == 0 && CN * kKC <= kThreads, "staging split");
+  const int tid = threadIdx.x;
+  const bool hasB = tid < CN * kKC;
+  const int cB = tid / kKC, kB = tid % kKC;
+  double va[NA], vb = 0.0;
+  auto fetch = [&](int kc) {
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      const int x = tid + kThreads * i, kk = x / RM, r = x % RM;
+      va[i] = A[(size_t)min(r0 + r, m - 1) + (size_t)min(kc + kk, K - 1) * lda];
+    }
+    if (hasB) vb = B[(size_t)min(kc + kB, K - 1) + (size_t)min(cb + cB, n - 1) * ldb];
+  };
   for (int kc = 0; kc < K; kc += kKC) {
     const int kn = min(kKC, K - kc);
-#pragma unroll 1
-    for (int x = threadIdx.x; x < kKC * RM; x += kThreads) {
-      const int kk = x / RM, r = x % RM;
-      tA[x] = (r0 + r < m && kk < kn) ? A[(size_t)(r0 + r) + (size_t)(kc + kk) * lda] : 0.0;
+    fetch(kc);
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      const int x = tid + kThreads * i, kk = x / RM, r = x % RM;
+      tA[x] = (r0 + r < m && kk < kn) ? va[i] : 0.0;
     }
-#pragma unroll 1
-    for (int x = threadIdx.x; x < CN * kKC; x += kThreads) {
-      const int c = x / kKC, kk = x % kKC;
-      tB[c * (kKC + 1) + kk] = (cb + c < n && kk < kn) ? B[(size_t)(kc + kk) + (size_t)(cb + c) * ldb] : 0.0;
-    }
+    if (hasB) tB[cB * (kKC + 1) + kB] = (cb + cB < n && kB < kn) ? vb : 0.0;
     __syncthreads();
 #pragma unroll 4
     for (int kk = 0; kk < kn; ++kk) {
