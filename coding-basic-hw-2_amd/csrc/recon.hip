@@ -72,8 +72,20 @@ __device__ __forceinline__ double fp64_dot(const oz2_problem& pr, int i, int j) 
   const GLOBAL double* a = gp(pr.A) + i;
   const GLOBAL double* b = gp(pr.B) + (size_t)j * pr.ldb;
   const size_t lda = (size_t)pr.lda;
+  const int K = pr.k;
   double s = 0.0;
-  for (int k = 0; k < pr.k; ++k) s = fma(a[(size_t)k * lda], b[k], s);
+  int k = 0;
+  for (; k + 8 <= K; k += 8) {   // 16 loads in flight, then the same fma chain
+    double x[8], y[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      x[t] = a[(size_t)(k + t) * lda];
+      y[t] = b[k + t];
+    }
+#pragma unroll
+    for (int t = 0; t < 8; ++t) s = fma(x[t], y[t], s);
+  }
+  for (; k < K; ++k) s = fma(a[(size_t)k * lda], b[k], s);
   return s;
 }
 
