@@ -109,12 +109,30 @@ def main():
 
     import torch
     if args.probe_copy:
+        # 5 timed copies (the counter calibration reads the copy dispatches only), then the stream
+        # rates a memory-bound kernel can reach on this GPU: read-only (a sum) and write-only (a fill)
         src = torch.ones(1 << 30, dtype=torch.uint8, device="cuda:0")
         dst = torch.empty_like(src)
-        for _ in range(5):
-            dst.copy_(src)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+        def rate(f, reps, nbytes):
+            e0.record()
+            for _ in range(reps):
+                f()
+            e1.record()
+            torch.cuda.synchronize()
+            return round(nbytes * reps / (e0.elapsed_time(e1) * 1e9), 3)
+
+        dst.copy_(src)
         torch.cuda.synchronize()
-        print(json.dumps({"probe": "copy", "bytes_read": 1 << 30, "bytes_written": 1 << 30, "launches": 5}))
+        copy_tb = rate(lambda: dst.copy_(src), 4, 2 << 30)
+        x = src.view(torch.float64)
+        y = dst.view(torch.float64)
+        x.sum()
+        read_tb = rate(lambda: x.sum(), 10, 1 << 30)
+        write_tb = rate(lambda: y.fill_(1.0), 10, 1 << 30)
+        print(json.dumps({"probe": "copy", "bytes_read": 1 << 30, "bytes_written": 1 << 30, "launches": 5,
+                          "copy_TB_s": copy_tb, "read_TB_s": read_tb, "write_TB_s": write_tb}))
         return
     import ggemm as G
 
