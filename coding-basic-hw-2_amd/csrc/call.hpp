@@ -29,7 +29,7 @@ struct GroupedCall {
   int i8_kernel = kI8General;     // INT8 GEMM kernel the schedule was built for
   bool blocked = false;           // digit and abs planes in the blocked layout
   bool packed = false;            // residue planes in the packed layout
-  int f64_tiles = 0;
+  int f64_tiles = 0;              // native GEMM launch word (tile count, kF64Tile128 for 128 x 128 tiles)
   size_t h2d_bytes = 0;           // bytes of the blob to copy
 };
 

@@ -145,10 +145,13 @@ struct YDesc {
   const int32_t* L;
 };
 
-// FP64 MFMA grouped GEMM (native routes).  h_ws receives the schedule image.
-int f64_build_schedule(const F64Problem* h, int num, void* h_ws, size_t ws_bytes, int* total_tiles,
-                       size_t* bytes_used);
-int f64_launch(const F64Problem* d_probs, const void* d_sched, int total_tiles, hipStream_t s);
+// FP64 MFMA grouped GEMM (native routes).  h_ws receives the schedule image; *launch receives the
+// launch word for f64_launch: the tile count in bits 0-29, kF64Tile128 set for 128 x 128 tiles (0:
+// nothing to launch).  tile_mode 0 chooses the tile edge from the group's shapes, 64 or 128 forces it.
+constexpr int kF64Tile128 = 1 << 30;
+int f64_build_schedule(const F64Problem* h, int num, void* h_ws, size_t ws_bytes, int* launch, size_t* bytes_used,
+                       int tile_mode = 0);
+int f64_launch(const F64Problem* d_probs, const void* d_sched, int launch, hipStream_t s);
 
 // Launchers used by the orchestration (return 0 on success).
 // fold_q != 0: the residues of A plane l are (q_l r) mod p_l (symmetric) instead of r, with q_l the
@@ -200,4 +203,5 @@ struct ggemm_handle_s {
   int digits_colmajor; // GGEMM_DIGITS_COLMAJOR=1 at create: row-major residues and column-major digits
   int i8_mode;         // GGEMM_I8_KERNEL at create: 0 automatic, 1 general kernel only, 2 large-tile kernel
                        // only, the kernel-level layouts (testing)
+  int f64_tile;        // GGEMM_F64_TILE at create: 0 automatic, 64 or 128 forces the native GEMM's tile edge
 };

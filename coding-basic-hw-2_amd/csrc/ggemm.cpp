@@ -317,7 +317,8 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
     }
   }
   for (int i = 0; i < c.nn; ++i) hf[i] = f64_of(probs[nat_idx[i]]);
-  if (c.nn && f64_build_schedule(hf, c.nn, hb + c.L.off_sf64, s_f64, &c.f64_tiles, nullptr)) return GGEMM_ERR_INVALID;
+  if (c.nn && f64_build_schedule(hf, c.nn, hb + c.L.off_sf64, s_f64, &c.f64_tiles, nullptr, h->f64_tile))
+    return GGEMM_ERR_INVALID;
   if (c.ne && i8_build_schedule(hi8, (int)c.n_i8, hb + c.L.off_si8, s_i8, &c.i8info, h->num_cus, large_mode(h, c),
                                    &c.i8_kernel))
     return GGEMM_ERR_I8GEMM;
@@ -407,7 +408,8 @@ int run_native(ggemm_handle_t h, const ggemm_problem_t* probs, const int* idx, i
   int* tl = grouped ? tiles : h->emu_idx;   // per-problem tile counts (host scratch)
   for (int i = 0; i < (grouped ? 1 : cnt); ++i) {
     const F64Problem* src = grouped ? hf : hf + i;
-    if (f64_build_schedule(src, grouped ? cnt : 1, hb + L.off_sf64 + (size_t)i * per, per, &tl[i], nullptr)) {
+    if (f64_build_schedule(src, grouped ? cnt : 1, hb + L.off_sf64 + (size_t)i * per, per, &tl[i], nullptr,
+                           h->f64_tile)) {
       release_slot(h, slot);
       return GGEMM_ERR_INVALID;
     }
@@ -686,6 +688,8 @@ extern "C" int ggemm_create_ex(ggemm_handle_t* out, int max_problems, size_t max
   h->digits_colmajor = (ec && std::atoi(ec) == 1) ? 1 : 0;
   const char* eg = std::getenv("GGEMM_I8_KERNEL");
   h->i8_mode = !eg ? 0 : !std::strcmp(eg, "general") ? 1 : !std::strcmp(eg, "large") ? 2 : 0;
+  const char* et = std::getenv("GGEMM_F64_TILE");
+  h->f64_tile = !et ? 0 : std::atoi(et) == 64 ? 64 : std::atoi(et) == 128 ? 128 : 0;
   const char* e = std::getenv("GGEMM_STATS_REPAIR");
   h->stats_repair = (e && std::atoi(e) == 1) ? 1 : 0;
   if (hipStreamSynchronize(stream) != hipSuccess) FAIL(GGEMM_ERR_CUDA);

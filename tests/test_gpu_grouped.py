@@ -385,6 +385,32 @@ def test_native_paths_gate(path):
     assert st.kernel_launches == (1 if path == G.PATH_NATIVE_GROUPED else 4)
 
 
+@pytest.mark.parametrize("path", [G.PATH_NATIVE_LOOP, G.PATH_NATIVE_GROUPED])
+@pytest.mark.parametrize("beta", [-0.5, 0.0])
+def test_native_tile_sizes_bitwise(path, beta):
+    """The native GEMM's 64 x 64 and 128 x 128 tile kernels (forced with GGEMM_F64_TILE) on the
+    same ragged group -- partial tiles on both edges, k not a multiple of the 16-deep stage, k = 0
+    and empty problems: every output bit equal (each entry takes the same k-ordered MFMA chain at
+    either size), each problem within the gamma_n gate of the host reference."""
+    shapes = [(300, 200, 77), (128, 128, 16), (129, 257, 300), (1, 1, 1), (33, 17, 0), (0, 5, 5), (260, 140, 1)]
+    outs = {}
+    for tile in ("64", "128"):
+        case = Case(shapes, 33, phi=1.0, alpha=1.5, beta=beta)
+        say(f"native path {path}, tile {tile}, beta {beta}")
+        with kernel_handle(case, None, GGEMM_F64_TILE=tile) as hd:
+            rc, st = run(case, path, CFG_EMU, handle=hd)
+        assert rc == 0
+        outs[tile] = [case.C(g).copy() for g in range(len(shapes))]
+        for g, h in enumerate(case.hp):
+            if h.m == 0 or h.n == 0:
+                continue
+            h.reference()
+            gate, _ = h.gate(case.C(g))
+            assert gate <= 1.0, (tile, g, gate)
+    for g in range(len(shapes)):
+        assert same_bits(outs["64"][g], outs["128"][g]), f"problem {g} {shapes[g]} differs between tile sizes"
+
+
 def test_bigk_fallback_and_unsafe():
     """k = 140000 > 131040: AUTO with fallback -> native route counted; allow_fallback = 0 ->
     GGEMM_ERR_UNSAFE (tests/test_grouped.cu:185-231)."""
