@@ -48,6 +48,8 @@
 #include "common.hpp"
 
 #define GGEMM_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+// output stores through global-address-space pointers (flat stores would also count in lgkmcnt)
+#define GLOBAL __attribute__((address_space(1)))
 
 namespace ggemm {
 namespace {
@@ -214,8 +216,8 @@ __device__ __forceinline__ uint32_t residue_byte(int32_t c, const I8Epi& e) {
 template <class C>
 __device__ __forceinline__ void store_blocked(const v4i (&acc)[C::FM][C::FN], const i8_problem& P, const I8Epi& epi,
                                               int kind, int bi0, int bj0, int mb, int lane) {
-  uint8_t* const y8 = reinterpret_cast<uint8_t*>(P.C) + 4 * lane;
-  int32_t* const y32 = reinterpret_cast<int32_t*>(P.C) + 4 * lane;
+  GLOBAL uint8_t* const y8 = ((GLOBAL uint8_t*)P.C) + 4 * lane;
+  GLOBAL int32_t* const y32 = ((GLOBAL int32_t*)P.C) + 4 * lane;
 #pragma unroll
   for (int j = 0; j < C::FN; ++j)
 #pragma unroll
@@ -225,7 +227,7 @@ __device__ __forceinline__ void store_blocked(const v4i (&acc)[C::FM][C::FN], co
       const size_t e0 = ((size_t)bj * mb + bi) * 256;
       const v4i v = acc[i][j];
       if (kind == 0) {
-        *reinterpret_cast<v4i*>(y32 + e0) = v;
+        *reinterpret_cast<GLOBAL v4i*>(y32 + e0) = v;
       } else {
         uint32_t y[4];
         if (kind == 1) {
@@ -237,7 +239,7 @@ __device__ __forceinline__ void store_blocked(const v4i (&acc)[C::FM][C::FN], co
         }
         const uint32_t lo = __builtin_amdgcn_perm(y[1], y[0], 0x0c0c0400u);
         const uint32_t hi = __builtin_amdgcn_perm(y[3], y[2], 0x0c0c0400u);
-        *reinterpret_cast<uint32_t*>(y8 + e0) = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+        *reinterpret_cast<GLOBAL uint32_t*>(y8 + e0) = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
       }
     }
 }
@@ -409,21 +411,21 @@ __device__ __forceinline__ void run_tile(uint8_t* lds, const i8_problem& P, cons
       if (col >= P.n || r0 >= P.m) continue;
       const v4i v = acc[i][j];
       if (!residue) {
-        int32_t* out = reinterpret_cast<int32_t*>(P.C) + (size_t)r0 + (size_t)col * ldc;
+        GLOBAL int32_t* out = ((GLOBAL int32_t*)P.C) + (size_t)r0 + (size_t)col * ldc;
         if (vec && r0 + 3 < P.m) {
-          *reinterpret_cast<v4i*>(out) = v;
+          *reinterpret_cast<GLOBAL v4i*>(out) = v;
         } else {
 #pragma unroll
           for (int r = 0; r < 4; ++r)
             if (r0 + r < P.m) out[r] = v[r];
         }
       } else {
-        uint8_t* out = reinterpret_cast<uint8_t*>(P.C) + (size_t)r0 + (size_t)col * ldc;
+        GLOBAL uint8_t* out = ((GLOBAL uint8_t*)P.C) + (size_t)r0 + (size_t)col * ldc;
         uint32_t y[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) y[r] = (epi.mode & kEpiAccBias) ? residue_byte<true>(v[r], epi) : residue_byte<false>(v[r], epi);
         if (vec && r0 + 3 < P.m) {
-          *reinterpret_cast<uint32_t*>(out) = y[0] | (y[1] << 8) | (y[2] << 16) | (y[3] << 24);
+          *reinterpret_cast<GLOBAL uint32_t*>(out) = y[0] | (y[1] << 8) | (y[2] << 16) | (y[3] << 24);
         } else {
 #pragma unroll
           for (int r = 0; r < 4; ++r)

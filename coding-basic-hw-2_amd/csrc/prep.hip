@@ -32,6 +32,13 @@
 
 #include "common.hpp"
 
+// global address space for every HBM access: the descriptor pointers would otherwise compile to
+// flat accesses, which also count in lgkmcnt, so the LDS waits of the reductions and of the
+// exchange row would wait for the HBM loads in flight as well
+#define GLOBAL __attribute__((address_space(1)))
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
 #pragma clang fp contract(off)
 
 namespace ggemm {
@@ -183,7 +190,7 @@ __device__ __forceinline__ void scaled(const double* x, int sh, double* out) {
 // two-word case.
 template <int NE, bool kWide>
 __device__ __forceinline__ void planes(const double* xt, int N, const CrtTables* __restrict__ tab, int widx,
-                                       int8_t* dst, size_t stride) {
+                                       GLOBAL int8_t* dst, size_t stride) {
   constexpr int P = (kWide && NE > 8) ? 8 : NE;   // values per pass
 #pragma unroll
   for (int h = 0; h < NE; h += P) {
@@ -193,13 +200,13 @@ __device__ __forceinline__ void planes(const double* xt, int N, const CrtTables*
     for (int l = 0; l < N; ++l) {
       uint32_t q[P / 4];
       residue_bytes<P, kWide>(x, plane_w<kWide>(tab, l, widx), q);
-      int8_t* d = dst + (size_t)l * stride + h;
+      GLOBAL int8_t* d = dst + (size_t)l * stride + h;
       if constexpr (P == 16)
-        *reinterpret_cast<uint4*>(d) = make_uint4(q[0], q[1], q[2], q[3]);
+        *(GLOBAL u32x4*)(d) = u32x4{q[0], q[1], q[2], q[3]};
       else if constexpr (P == 8)
-        *reinterpret_cast<uint2*>(d) = make_uint2(q[0], q[1]);
+        *(GLOBAL u32x2*)(d) = u32x2{q[0], q[1]};
       else
-        *reinterpret_cast<uint32_t*>(d) = q[0];
+        *(GLOBAL uint32_t*)(d) = q[0];
     }
   }
 }
@@ -226,7 +233,7 @@ __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ t
   const int r = tid & 31, c = tid >> 5;          // chain role: row r, chain c
   const int i = row0 + r;
   const bool valid = i < m;
-  const double* __restrict__ A = pr.A;
+  const GLOBAL double* __restrict__ A = (const GLOBAL double*)pr.A;
   const size_t lda = (size_t)pr.lda;
   const double T = tab->T[N];
 
@@ -278,8 +285,8 @@ __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ t
     sm.shift[r] = sh;
     sm.sig[r] = sg;
     if (valid && split == 0) {
-      pr.row_shift[i] = sh;
-      pr.row_shift[m + i] = sg;
+      ((GLOBAL int32_t*)pr.row_shift)[i] = sh;
+      ((GLOBAL int32_t*)pr.row_shift)[m + i] = sg;
       if (sh == OZ2_SHIFT_NONFINITE) atomicAdd(&cnt[0], 1ull);
     }
   }
@@ -322,10 +329,10 @@ __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ t
     __syncthreads();
     const int kb = k0 + 16 * seg;
     if (t >= w0 && t < w1 && rvalid && kb < Kp) {
-      int8_t* dst = pr.A8 + (packed ? packed_offset(row0 + rr, kb, m, Kp) : (size_t)(row0 + rr) * Kp + kb);
+      GLOBAL int8_t* dst = (GLOBAL int8_t*)pr.A8 + (packed ? packed_offset(row0 + rr, kb, m, Kp) : (size_t)(row0 + rr) * Kp + kb);
       if (nf_r) {
         for (int l = 0; l <= N; ++l)
-          *reinterpret_cast<uint4*>(dst + (size_t)l * pr.a8_mod_stride) = make_uint4(0u, 0u, 0u, 0u);
+          *(GLOBAL u32x4*)(dst + (size_t)l * pr.a8_mod_stride) = u32x4{0u, 0u, 0u, 0u};
       } else {
         double av[16], xt[16];
 #pragma unroll
@@ -337,7 +344,7 @@ __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ t
 #pragma unroll
           for (int e = 0; e < 4; ++e) q[w] |= abs_u8(av[4 * w + e], sg_r) << (8 * e);
         }
-        *reinterpret_cast<uint4*>(dst + (size_t)N * pr.a8_mod_stride) = make_uint4(q[0], q[1], q[2], q[3]);
+        *(GLOBAL u32x4*)(dst + (size_t)N * pr.a8_mod_stride) = u32x4{q[0], q[1], q[2], q[3]};
         scaled<16>(av, sh_r, xt);
 #pragma unroll
         for (int e = 0; e < 16; ++e) xt[e] = trunc(xt[e]);
@@ -353,8 +360,8 @@ __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ t
   if (c == 0 && valid) {
     double D = 0.0, Nn = 0.0;
     for (int q = 0; q < kChains; ++q) { D += sm.red0[q][r]; Nn += sm.red1[q][r]; }
-    pr.row_shift[2 * m + i] = norm_ub_bits(D);
-    pr.row_shift[3 * m + i] = norm_ub_bits(Nn);
+    ((GLOBAL int32_t*)pr.row_shift)[2 * m + i] = norm_ub_bits(D);
+    ((GLOBAL int32_t*)pr.row_shift)[3 * m + i] = norm_ub_bits(Nn);
   }
 }
 
@@ -368,7 +375,7 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
   const int j = blk * kBCols + w;
   const int n = pr.n, N = pr.num_moduli, K = pr.k, Kp = pr.kp;
   if (j >= n) return;   // no barriers below; the 32-lane group is column-uniform
-  const double* __restrict__ b = pr.B + (size_t)j * pr.ldb;
+  const GLOBAL double* __restrict__ b = (const GLOBAL double*)pr.B + (size_t)j * pr.ldb;
   const double T = tab->T[N];
 
   // K <= 32 kBReg: the column is read once; lane l keeps k = l + 32 t in registers (its norm chain,
@@ -428,14 +435,14 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
   const int sh = shift_from_norm(mx, ss, resc, T);
   const int sg = abs_shift(mx, sh);
   if (lane == 0 && split == 0) {
-    pr.col_shift[j] = sh;
-    pr.col_shift[n + j] = sg;
+    ((GLOBAL int32_t*)pr.col_shift)[j] = sh;
+    ((GLOBAL int32_t*)pr.col_shift)[n + j] = sg;
     if (sh == OZ2_SHIFT_NONFINITE) atomicAdd(&cnt[0], 1ull);
   }
   const bool nf = sh == OZ2_SHIFT_NONFINITE;
 
   double da2 = 0.0, na2 = 0.0;
-  int8_t* const B8 = pr.B8;
+  GLOBAL int8_t* const B8 = (GLOBAL int8_t*)pr.B8;
   const int nchunk = (Kp + 127) / 128;
   const int per = (nchunk + nsplit - 1) / nsplit;
   const int c0 = min(nchunk, split * per), c1 = min(nchunk, c0 + per);
@@ -445,11 +452,11 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
   auto chunk = [&](int ch, const double (&a)[4]) {
     const int k0 = 128 * ch + 4 * lane;
     if (k0 >= Kp) return;
-    int8_t* const base = B8 + (packed ? packed_offset(j, k0, n, Kp) : (size_t)j * Kp + k0);
+    GLOBAL int8_t* const base = B8 + (packed ? packed_offset(j, k0, n, Kp) : (size_t)j * Kp + k0);
     const bool write = ch >= c0 && ch < c1;
     if (nf) {
       if (write)
-        for (int l = 0; l <= N; ++l) *reinterpret_cast<uint32_t*>(base + (size_t)l * pr.b8_mod_stride) = 0u;
+        for (int l = 0; l <= N; ++l) *(GLOBAL uint32_t*)(base + (size_t)l * pr.b8_mod_stride) = 0u;
       return;
     }
     double xs[4], xt[4];
@@ -468,7 +475,7 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
     uint32_t q = 0u;
 #pragma unroll
     for (int e = 0; e < 4; ++e) q |= abs_u8(a[e], sg) << (8 * e);
-    *reinterpret_cast<uint32_t*>(base + (size_t)N * pr.b8_mod_stride) = q;
+    *(GLOBAL uint32_t*)(base + (size_t)N * pr.b8_mod_stride) = q;
   };
   const int ch0 = split == 0 ? 0 : c0, ch1 = split == 0 ? nchunk : c1;   // chunks walked here
   if (single) {
@@ -507,8 +514,8 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
     na2 += __shfl_xor(na2, o, 32);
   }
   if (lane == 0) {
-    pr.col_shift[2 * n + j] = norm_ub_bits(da2);
-    pr.col_shift[3 * n + j] = norm_ub_bits(na2);
+    ((GLOBAL int32_t*)pr.col_shift)[2 * n + j] = norm_ub_bits(da2);
+    ((GLOBAL int32_t*)pr.col_shift)[3 * n + j] = norm_ub_bits(na2);
   }
 }
 
