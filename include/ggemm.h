@@ -5,7 +5,7 @@
  * Drop-in C ABI for the reference's include/ggemm.h:1-90.  Every type, field, enum value and
  * function below keeps the reference's name, order and meaning; the only change is the stream
  * type (hipStream_t, pointer-sized like cudaStream_t).  The GGEMM_ERR_* return codes, private in
- * the reference (src/internal.h:155-165), are part of this ABI with the same values.
+ * the reference (src/internal.h:65-75), are part of this ABI with the same values.
  */
 #ifndef GGEMM_H
 #define GGEMM_H
@@ -70,7 +70,7 @@ typedef struct {
   long long num_safety_fallback;  /* entries computed in FP64 because of NaN/Inf input */
 } ggemm_stats_t;
 
-/* src/internal.h:155-165 (values unchanged) */
+/* src/internal.h:65-75 (values unchanged) */
 enum {
   GGEMM_OK = 0,
   GGEMM_ERR_INVALID = 1,    /* bad args / null handle / num_problems > max_problems */

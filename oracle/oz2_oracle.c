@@ -558,7 +558,7 @@ int oz2o_route_is_fallback(int r) {
 }
 static int tile_dim(int cfg) { return cfg == 0 ? 128 : (cfg == 1 ? 64 : 32); }
 static double rup(double x, double q) { return ceil(x / q) * q; }
-/* src/planner.cpp:237-246 */
+/* src/planner.cpp:153-168 (tile_by_padding, tiles_of) */
 static int tile_by_padding(int m, int n) {
   int best = 2;
   double best_eff = -1;
@@ -574,7 +574,7 @@ static double tiles_of(int m, int n, int cfg) {
   const double td = tile_dim(cfg);
   return ceil(m / td) * ceil(n / td);
 }
-/* src/planner.cpp:259-285 */
+/* src/planner.cpp:170-202 (constants and cost) */
 static void cost(const oz2o_shape* p, int nm, int cfg, const oz2o_device_model* dm, double* t_emu,
                  double* t_nat) {
   static const double eff[3] = {1.0, 0.63, 0.30};
@@ -591,7 +591,7 @@ static void cost(const oz2o_shape* p, int nm, int cfg, const oz2o_device_model* 
   const double nat_m = (m * k + k * n + c_rw * m * n) * 8 / dm->mem_bw;
   *t_nat = nat_c > nat_m ? nat_c : nat_m;
 }
-/* src/planner.cpp:291-314 */
+/* src/planner.cpp:204-231 (tune_tiles) */
 static int tune_tiles(const oz2o_shape* probs, int num, const oz2o_device_model* dm, oz2o_plan_entry* out) {
   const double slots = (double)dm->num_sms * 2;
   int any = 0;
@@ -616,7 +616,7 @@ static int tune_tiles(const oz2o_shape* probs, int num, const oz2o_device_model*
   }
   return any;
 }
-/* src/planner.cpp:221-231 */
+/* src/planner.cpp:137-148 (ggemm_plan_num_moduli) */
 static int plan_num_moduli(int cfg_nm, double target, int k) {
   int nm;
   if (cfg_nm > 0) {
@@ -627,7 +627,8 @@ static int plan_num_moduli(int cfg_nm, double target, int k) {
   }
   return nm < 2 ? 2 : (nm > OZ2O_MAX_MODULI ? OZ2O_MAX_MODULI : nm);
 }
-/* src/planner.cpp:319-346 and 369-413 (without the shape memo, which is bit-identical) */
+/* src/planner.cpp:236-263 (plan_shape) and 286-330 (ggemm_plan_ex, without the shape memo, which is
+   bit-identical) */
 int oz2o_plan(const oz2o_shape* probs, int num, int cfg_nm, double target, int allow_fb, int path,
               const oz2o_device_model* dm, double rho, oz2o_plan_entry* out) {
   const int autop = (path == 4);

@@ -8,9 +8,12 @@ Writes tests/golden/numerics_kat.json with
   * "log2P", "bound_k1024": per N = 8..20 (log lines 4-16),
   * "choose_1e15": oz2_choose_num_moduli(k, 1e-15) for six k (log line 17),
   * "sweep": per (m, n, k, phi) the naive-FP64 rel_cw of the generated data and, per N,
-    the repaired-entry count "rep" (log lines 23-340),
-  * "grouped_repaired", "nonfinite_counter", "repair_modes": the single-number KATs of
-    sections 3-5 (log lines 343, 355, 357).
+    the repaired-entry count "rep" and the printed error columns "cols" = [rel_cw, rel_abs,
+    rel_nrm, bound, gate] (log lines 23-340),
+  * "grouped_repaired" and "grouped": the 9-problem launch's repair total and, per problem,
+    (m, n, k, N) with the same five columns (log lines 343-353),
+  * "nonfinite_counter", "nonfinite_gate": section 4 (log line 355),
+  * "repair_modes": section 5's counts, OFF == COUNT flag and the OFF / COUNT / ON gates (log line 357).
 Run: python tests/golden/extract_numerics_kat.py [path/to/log]
 """
 import json
@@ -45,20 +48,30 @@ def main():
                    "phi": float(m.group(4)), "naive_rel_cw": float(m.group(5)), "rep": {}}
             out["sweep"].append(cur)
             continue
-        m = re.match(r"^\s*(\d+)\s+[\d.e+-]+\s+[\d.e+-]+\s+[\d.e+-]+\s+[\d.e+-]+\s+[\d.e+-]+\s+(\d+)\s+ok", ln)
+        m = re.match(r"^\s*(\d+)\s+([\d.e+-]+)\s+([\d.e+-]+)\s+([\d.e+-]+)\s+([\d.e+-]+)\s+([\d.e+-]+)\s+(\d+)\s+ok", ln)
         if m and cur is not None:
-            cur["rep"][m.group(1)] = int(m.group(2))
+            cur["rep"][m.group(1)] = int(m.group(7))
+            cur.setdefault("cols", {})[m.group(1)] = [float(m.group(q)) for q in range(2, 7)]
+            continue
+        m = re.match(r"^\s*(\d+)\s+(\d+)\s+(\d+)\s+(\d+)\s+([\d.e+-]+)\s+([\d.e+-]+)\s+([\d.e+-]+)\s+"
+                     r"([\d.e+-]+)\s+([\d.e+-]+)\s+ok$", ln)
+        if m and "grouped_repaired" in out:
+            out.setdefault("grouped", []).append({"mnkN": [int(m.group(q)) for q in range(1, 5)],
+                                                  "cols": [float(m.group(q)) for q in range(5, 10)]})
             continue
         m = re.match(r"^grouped launch .* total repaired entries=(\d+)", ln)
         if m:
             out["grouped_repaired"] = int(m.group(1))
-        m = re.match(r"^non-finite: counter=(\d+)", ln)
+        m = re.match(r"^non-finite: counter=(\d+) .* gate\(rest\)=([\d.e+-]+)", ln)
         if m:
             out["nonfinite_counter"] = int(m.group(1))
-        m = re.match(r"^repair modes .* uncertified=(\d+) .* repaired=(\d+) \| OFF==COUNT bitwise:(\d)", ln)
+            out["nonfinite_gate"] = float(m.group(2))
+        m = re.match(r"^repair modes .* OFF gate=([\d.e+-]+) \| COUNT gate=([\d.e+-]+) uncertified=(\d+) \| "
+                     r"ON gate=([\d.e+-]+) repaired=(\d+) \| OFF==COUNT bitwise:(\d)", ln)
         if m:
-            out["repair_modes"] = {"uncertified": int(m.group(1)), "repaired": int(m.group(2)),
-                                   "off_eq_count": int(m.group(3))}
+            out["repair_modes"] = {"uncertified": int(m.group(3)), "repaired": int(m.group(5)),
+                                   "off_eq_count": int(m.group(6)),
+                                   "gates": [float(m.group(1)), float(m.group(2)), float(m.group(4))]}
     dst = Path(__file__).with_name("numerics_kat.json")
     dst.write_text(json.dumps(out, indent=1) + "\n")
     print(f"wrote {dst}: {len(out['sweep'])} sweep cases")

@@ -9,6 +9,7 @@
 // (k rows of n columns, ldb = k + 3), then C0 (m rows of n columns, ldc = m + 1) with phi = 0.
 // Replaying the same calls in the same order through libstdc++ gives the same doubles, which the
 // logged "naive FP64 dot rel_cw" values (log lines 23-327) confirm case by case.
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstring>
@@ -143,6 +144,48 @@ double katgen_gate(int m, int n, int k, double alpha, double beta, const double*
     }
   if (over) *over = cnt;
   return gate;
+}
+
+// The four error columns the reference test prints per problem (tests/test_numerics_standalone.cu:
+// 180-206, check()): out[0] rel_cw = max |C - R| / |R| (R != 0), out[1] rel_abs and out[2] rel_nrm =
+// max err_ab / (|alpha| absAB) and / (|alpha| nrm) with err_ab = max(0, |C - R| - 4u(|beta C0| + |R|)),
+// out[3] gate = max |C - R| / (gamma_n (|alpha| absAB + |beta C0|)).  Running maxima use std::max,
+// so a NaN candidate never replaces the maximum.  Returns 1 when the padding rows i in [m, ldc) of
+// C equal those of C0 (the test's beta_ok), else 0.
+int katgen_check(int m, int n, int k, double alpha, double beta, const double* C, const double* C0, int ldc,
+                 const long double* R, const double* absAB, const double* nrm, double* out) {
+  double nn = (double)k + (alpha != 1.0) + (beta != 0.0);
+  if (nn < 1) nn = 1;
+  const double u = std::ldexp(1.0, -53);
+  const double gam = nn * u / (1.0 - nn * u);
+  double cw = 0, ab = 0, nr = 0, gate = 0;
+  int beta_ok = 1;
+  for (int j = 0; j < n; ++j) {
+    for (int i = 0; i < m; ++i) {
+      const long double r = R[i + (size_t)j * m];
+      const double c = C[i + (size_t)j * ldc];
+      const double c0 = C0[i + (size_t)j * ldc];
+      const long double err = fabsl((long double)c - r);
+      const long double slack = 4.0L * ldexpl(1.0L, -53) * (fabsl((long double)beta * c0) + fabsl(r));
+      const long double err_ab = err > slack ? err - slack : 0.0L;
+      if (r != 0) cw = std::max(cw, (double)(err / fabsl(r)));
+      const double sa = std::fabs(alpha) * absAB[i + (size_t)j * m];
+      const double sn = std::fabs(alpha) * nrm[i + (size_t)j * m];
+      if (sa > 0) ab = std::max(ab, (double)(err_ab / sa));
+      if (sn > 0) nr = std::max(nr, (double)(err_ab / sn));
+      else if (err_ab > 0) nr = INFINITY;
+      const long double den = gam * ((long double)sa + fabsl((long double)beta * c0));
+      if (den > 0) gate = std::max(gate, (double)(err / den));
+      else if (err > 0) gate = INFINITY;
+    }
+    for (int i = m; i < ldc; ++i)
+      if (C[i + (size_t)j * ldc] != C0[i + (size_t)j * ldc]) beta_ok = 0;
+  }
+  out[0] = cw;
+  out[1] = ab;
+  out[2] = nr;
+  out[3] = gate;
+  return beta_ok;
 }
 
 }  // extern "C"

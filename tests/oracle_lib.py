@@ -104,6 +104,8 @@ def katgen():
                                             C.c_int, C.c_double, C.c_double, _dp, _dp, _dp, _dp]
         lib.katgen_naive_relcw.restype = C.c_double
         lib.katgen_naive_relcw.argtypes = [C.c_int, C.c_int, C.c_int, _dp, C.c_int, _dp, C.c_int, _ldp]
+        lib.katgen_check.argtypes = [C.c_int, C.c_int, C.c_int, C.c_double, C.c_double, _dp, _dp, C.c_int,
+                                     _ldp, _dp, _dp, _dp]
         lib.katgen_gate.restype = C.c_double
         lib.katgen_gate.argtypes = [C.c_int, C.c_int, C.c_int, C.c_double, C.c_double, _dp, C.c_int,
                                     _dp, C.c_int, _ldp, _dp, C.POINTER(C.c_longlong)]
@@ -149,6 +151,14 @@ class HostProb:
         g = katgen().katgen_gate(self.m, self.n, self.k, self.alpha, self.beta, Cres, self.ldc, self.C0,
                                  self.ldc, self.R, self.absAB, C.byref(cnt))
         return g, cnt.value
+
+    def check(self, Cres):
+        """The reference test's error columns of Cres (ldc layout) against R (after reference()):
+        (rel_cw, rel_abs, rel_nrm, gate), and whether C's padding rows equal C0's."""
+        out = np.zeros(4)
+        ok = katgen().katgen_check(self.m, self.n, self.k, self.alpha, self.beta, np.ascontiguousarray(Cres),
+                                   self.C0, self.ldc, self.R, self.absAB, self.nrm, out)
+        return tuple(float(x) for x in out), bool(ok)
 
     def emulate(self, mode=REPAIR_ON, N=None):
         """Oracle result C (ldc layout) and counters [nonfinite, uncertified, repaired, safety]."""

@@ -198,7 +198,9 @@ PHIS = [0.0, 0.5, 1.0, 2.0, 4.0]
 
 def test_sweep_repair_count_kats():
     """log lines 23-340: for every (shape, phi) the replayed data reproduces the logged naive FP64
-    rel_cw, and the oracle's repaired-entry count matches the log for every N = 8..20."""
+    rel_cw, and the oracle's repaired-entry count and its four error columns (rel_cw, rel_abs,
+    rel_nrm, gate) match the log for every N = 8..20 checked."""
+    ora = oracle()
     _replay_prefix()
     ci = 0
     for sh in SWEEP_SHAPES:
@@ -214,6 +216,12 @@ def test_sweep_repair_count_kats():
                 assert int(cnt[2]) == exp["rep"][str(N)], (sh, phi, N)
                 g, over = h.gate(Cres)
                 assert g <= 1.0 and over == 0, (sh, phi, N, g)
+                # every printed column to the log's 4 significant digits: the worst entry's error
+                # (rel_cw, rel_abs, rel_nrm, gate) moves with any bit of any emulated entry
+                cols, beta_ok = h.check(Cres)
+                got = list(cols[:3]) + [ora.oz2o_error_bound(sh[2], N), cols[3]]
+                assert beta_ok, (sh, phi, N)
+                assert [f"{x:.3e}" for x in got] == [f"{x:.3e}" for x in exp["cols"][str(N)]], (sh, phi, N)
 
 
 def _advance_to_section3():
@@ -266,30 +274,51 @@ def make_section5():
 
 
 def test_grouped_and_nonfinite_kats():
+    """log lines 343-355: the 9-problem launch's repair total and, per problem, the four error
+    columns and the a-priori bound to the printed digits; the non-finite problem's counter, its
+    poisoned row / column, and the gate over the other entries."""
     hs, h4 = make_section4()
     total = 0
-    for h in hs:
+    for h, exp in zip(hs, KAT["grouped"]):
+        assert [h.m, h.n, h.k, h.N] == exp["mnkN"]
         Cres, cnt = h.emulate(REPAIR_ON)
         total += int(cnt[2])
         g, over = h.gate(Cres)
         assert g <= 1.0
+        cols, beta_ok = h.check(Cres)
+        got = list(cols[:3]) + [oracle().oz2o_error_bound(h.k, h.N), cols[3]]
+        assert beta_ok
+        assert [f"{x:.3e}" for x in got] == [f"{x:.3e}" for x in exp["cols"]], exp["mnkN"]
     assert total == KAT["grouped_repaired"]
     Cres, cnt = h4.emulate(REPAIR_ON)
     assert int(cnt[0]) == KAT["nonfinite_counter"]
     Cm = Cres.reshape(h4.n, h4.ldc)[:, :h4.m].T
     assert not np.isfinite(Cm[2, :]).any() and not np.isfinite(Cm[:, 4]).any()
+    # gate(rest): err / (gamma_n |A||B|) over the entries outside row 2 and column 4, with R and
+    # |A||B| of the data before the NaN / Inf were planted (tests/test_numerics_standalone.cu:368-398)
+    u = 2.0 ** -53
+    gam = h4.k * u / (1 - h4.k * u)
+    R = h4.R.reshape(h4.n, h4.m).T
+    ab = h4.absAB.reshape(h4.n, h4.m).T
+    keep = np.ones((h4.m, h4.n), dtype=bool)
+    keep[2, :] = False
+    keep[:, 4] = False
+    gate = float(np.max(np.abs(Cm[keep].astype(np.longdouble) - R[keep]) / (gam * ab[keep])))
+    assert f"{gate:.3e}" == f"{KAT['nonfinite_gate']:.3e}"
 
 
 def test_repair_mode_kats():
     hs = make_section5()
-    outs, cnts = {}, {}
+    outs, cnts, gates = {}, {}, []
     for mode in (REPAIR_OFF, REPAIR_COUNT, REPAIR_ON):
         res = [h.emulate(mode) for h in hs]
         outs[mode] = np.concatenate([r[0] for r in res])
         cnts[mode] = sum(r[1] for r in res)
         gmax = max(h.gate(r[0])[0] for h, r in zip(hs, res))
+        gates.append(max(h.check(r[0])[0][3] for h, r in zip(hs, res)))
         if mode == REPAIR_ON:
             assert gmax <= 1.0
+    assert [f"{x:.3e}" for x in gates] == [f"{x:.3e}" for x in KAT["repair_modes"]["gates"]]
     assert int(cnts[REPAIR_COUNT][1]) == KAT["repair_modes"]["uncertified"]
     assert int(cnts[REPAIR_ON][2]) == KAT["repair_modes"]["repaired"]
     assert np.array_equal(outs[REPAIR_OFF].view(np.int64), outs[REPAIR_COUNT].view(np.int64))
