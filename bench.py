@@ -1,14 +1,21 @@
 """Benchmark: grouped Ozaki-II FP64 GEMM (INT8 MFMA emulation) on one MI355X.
 
-Metric: effective FP64 TFLOP/s = sum_g 2 m_g n_g k_g / t, t = wall time of one
-ggemm_grouped_dgemm call (hipEvent-bracketed over K back-to-back calls on the handle's stream,
-inputs resident in HBM), reported with % of the INT8 MFMA peak, % of the FP64 MFMA peak and the
-max certified error (sampled entries vs an 80-bit host reference).
+Metric: effective FP64 TFLOP/s = sum_g 2 m_g n_g k_g / t, t = time of one run (hipEvent-bracketed
+over K back-to-back runs on the handle's stream, inputs resident in HBM), reported with the
+fraction of the INT8 MFMA peak, of the FP64 MFMA peak, and the max certified error of sampled
+entries (against an 80-bit host dot; the same entries also compared bit for bit with the CPU
+oracle's emulation).
 
-Default workload = the uniform group G=64, m=n=k=1024, entries (U-0.5) exp(0.5 Z), alpha=1,
-beta=0.5 with random C, adaptive moduli at 1e-15, fallback allowed, repair ON, through the
-grouped emulation path (GGEMM_PATH_EMU_GROUPED).  --workload large runs G=8 x 8192 x 8192 x 16384.
-Prints ONE JSON line.
+Workloads (--workload):
+  large    (default) G=8, m=n=8192, k=16384, U(-1,1), alpha=1, beta=0, adaptive N at 1e-15
+           (EMU_GROUPED: N=16), repeated via plan/execute (a hipGraph made once) with the pointers
+           updated between runs -- alternating two output buffers;
+  uniform  G=64, m=n=k=1024, (U-0.5)exp(0.5Z), alpha=1, beta=0.5 with random C, EMU_GROUPED;
+  ragged   G=128, m, n log-uniform in [64, 4096], k log-uniform in [16, 8192], (U-0.5)exp(Z),
+           alpha ~ U(-2,2) with 8 alpha = 0, beta ~ U(-1,1), create_ex(min_k = 16), EMU_GROUPED;
+  hard     G=32 x 2048^3 + 4 x 2048^2 x 65536, (U-0.5)exp(4Z), 0.1 % NaN/+-Inf entries, AUTO;
+  plumbing G=1, 256^3, U(-0.5,0.5), fixed N=14.
+Every run uses repair ON.  Prints ONE JSON line.
 """
 import argparse
 import ctypes as C
@@ -28,15 +35,39 @@ FP64_PEAK_TFLOPS = 78.6     # MI355X FP64 MFMA, TFLOP/s
 HBM_PEAK_GBS = 8000.0
 
 WORKLOADS = {
-    # name: (G, m, n, k, phi, alpha, beta, seed offset, path)
-    "uniform": dict(G=64, m=1024, n=1024, k=1024, phi=0.5, alpha=1.0, beta=0.5, seed=1,
-                    desc="uniform group G=64, m=n=k=1024, (U-0.5)exp(0.5Z), alpha=1, beta=0.5, adaptive N at 1e-15"),
-    "large": dict(G=8, m=8192, n=8192, k=16384, phi=0.0, alpha=1.0, beta=0.0, seed=3, graph=True,
-                  desc="large group G=8, m=n=8192, k=16384, U(-1,1), alpha=1, beta=0, adaptive N at 1e-15, "
-                       "repeated via plan/execute (hipGraph) with pointer updates between runs"),
-    "plumbing": dict(G=1, m=256, n=256, k=256, phi=0.0, alpha=1.0, beta=0.0, seed=0,
-                     desc="single 256^3, U(-0.5,0.5), fixed N=14"),
+    "large": dict(desc="large group G=8, m=n=8192, k=16384, U(-1,1), alpha=1, beta=0, adaptive N at 1e-15, "
+                       "repeated via plan/execute (hipGraph) with pointer updates between runs",
+                  seed=3, graph=True, path="EMU_GROUPED"),
+    "uniform": dict(desc="uniform group G=64, m=n=k=1024, (U-0.5)exp(0.5Z), alpha=1, beta=0.5, adaptive N at 1e-15",
+                    seed=1, path="EMU_GROUPED"),
+    "ragged": dict(desc="ragged group G=128, m,n log-U[64,4096], k log-U[16,8192], (U-0.5)exp(Z), alpha~U(-2,2) "
+                        "with 8 alpha=0, beta~U(-1,1), adaptive N at 1e-15, create_ex(min_k=16)",
+                   seed=2, path="EMU_GROUPED", min_k=16),
+    "hard": dict(desc="hard numerics G=32 x 2048^3 + 4 x 2048^2 x 65536, (U-0.5)exp(4Z), 0.1% NaN/+-Inf, AUTO, "
+                      "repair on", seed=4, path="AUTO"),
+    "plumbing": dict(desc="single 256^3, U(-0.5,0.5), fixed N=14", seed=0, path="EMU_GROUPED", fixed_n=14),
 }
+
+
+def shapes_of(name):
+    """[(m, n, k, alpha, beta, phi, lo_hi, nonfinite_rate)] of a workload."""
+    if name == "large":
+        return [(8192, 8192, 16384, 1.0, 0.0, 0.0, (-1.0, 1.0), 0.0)] * 8
+    if name == "uniform":
+        return [(1024, 1024, 1024, 1.0, 0.5, 0.5, None, 0.0)] * 64
+    if name == "plumbing":
+        return [(256, 256, 256, 1.0, 0.0, 0.0, (-0.5, 0.5), 0.0)]
+    if name == "hard":
+        return [(2048, 2048, 2048, 1.0, 0.0, 4.0, None, 1e-3)] * 32 + [(2048, 2048, 65536, 1.0, 0.0, 4.0, None, 1e-3)] * 4
+    rng = np.random.default_rng(20261203)   # ragged
+    lu = lambda lo, hi: int(np.exp(rng.uniform(np.log(lo), np.log(hi))))
+    zero = set(rng.choice(128, 8, replace=False).tolist())
+    out = []
+    for g in range(128):
+        m, n, k = lu(64, 4096), lu(64, 4096), lu(16, 8192)
+        a = 0.0 if g in zero else float(rng.uniform(-2, 2))
+        out.append((m, n, k, a, float(rng.uniform(-1, 1)), 1.0, None, 0.0))
+    return out
 
 
 def splitmix_uniform(torch, seed, count, device, salt):
@@ -54,8 +85,9 @@ def splitmix_uniform(torch, seed, count, device, salt):
     return srl(z, 11).to(torch.float64) * 2.0 ** -53
 
 
-def fill(torch, out, phi, seed, salt, lo_hi=None):
-    """(U - 0.5) exp(phi Z) with Z from Box-Muller; lo_hi=(a, b) gives U(a, b) instead."""
+def fill(torch, out, phi, seed, salt, lo_hi=None, nonfinite=0.0):
+    """(U - 0.5) exp(phi Z) with Z from Box-Muller; lo_hi=(a, b) gives U(a, b) instead; a fraction
+    `nonfinite` of the entries replaced by NaN, +Inf or -Inf (a fourth and fifth stream)."""
     n = out.numel()
     step = 1 << 26
     for s0 in range(0, n, step):
@@ -70,6 +102,11 @@ def fill(torch, out, phi, seed, salt, lo_hi=None):
                 u2 = splitmix_uniform(torch, seed + s0 * 7, cnt, out.device, salt + 2)
                 z = torch.sqrt(-2.0 * torch.log(u1)) * torch.cos(2 * np.pi * u2)
                 v = v * torch.exp(phi * z)
+        if nonfinite:
+            w = splitmix_uniform(torch, seed + s0 * 7, cnt, out.device, salt + 3)
+            kind = (splitmix_uniform(torch, seed + s0 * 7, cnt, out.device, salt + 4) * 3).to(torch.int64)
+            vals = torch.tensor([float("nan"), float("inf"), float("-inf")], dtype=torch.float64, device=out.device)
+            v = torch.where(w < nonfinite, vals[kind], v)
         out.view(-1)[s0:s0 + cnt] = v
 
 
@@ -91,14 +128,64 @@ def kp_of(k):
     return (k + 31) // 32 * 32
 
 
+def host_cpu():
+    """CPU model, the affinity mask as ranges and the logical CPU count of this host."""
+    model = "unknown"
+    try:
+        for ln in Path("/proc/cpuinfo").read_text().splitlines():
+            if ln.startswith("model name"):
+                model = ln.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    cpus = sorted(os.sched_getaffinity(0))
+    runs, start = [], None
+    for i, c in enumerate(cpus):
+        if start is None:
+            start = c
+        if i + 1 == len(cpus) or cpus[i + 1] != c + 1:
+            runs.append(f"{start}-{c}" if c != start else f"{c}")
+            start = None
+    return model, ",".join(runs), os.cpu_count(), len(cpus)
+
+
+def probe_copy(torch):
+    """5 timed 1 GiB device copies (the counter calibration reads the copy dispatches only), then the
+    stream rates a memory-bound kernel can reach on this GPU: read-only (a sum), write-only (a fill)."""
+    src = torch.ones(1 << 30, dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def rate(f, reps, nbytes):
+        e0.record()
+        for _ in range(reps):
+            f()
+        e1.record()
+        torch.cuda.synchronize()
+        return round(nbytes * reps / (e0.elapsed_time(e1) * 1e9), 3)
+
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    copy_tb = rate(lambda: dst.copy_(src), 4, 2 << 30)
+    x = src.view(torch.float64)
+    y = dst.view(torch.float64)
+    x.sum()
+    read_tb = rate(lambda: x.sum(), 10, 1 << 30)
+    write_tb = rate(lambda: y.fill_(1.0), 10, 1 << 30)
+    print(json.dumps({"probe": "copy", "bytes_read": 1 << 30, "bytes_written": 1 << 30, "launches": 5,
+                      "copy_TB_s": copy_tb, "read_TB_s": read_tb, "write_TB_s": write_tb}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="uniform", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="large", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-native", action="store_true")
+    ap.add_argument("--no-validate", action="store_true",
+                    help="skip the oracle / counter validation after the timed region")
     ap.add_argument("--probe-copy", action="store_true",
                     help="only run a plain 1 GiB device copy 5 times (calibrates the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
@@ -109,58 +196,37 @@ def main():
 
     import torch
     if args.probe_copy:
-        # 5 timed copies (the counter calibration reads the copy dispatches only), then the stream
-        # rates a memory-bound kernel can reach on this GPU: read-only (a sum) and write-only (a fill)
-        src = torch.ones(1 << 30, dtype=torch.uint8, device="cuda:0")
-        dst = torch.empty_like(src)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-
-        def rate(f, reps, nbytes):
-            e0.record()
-            for _ in range(reps):
-                f()
-            e1.record()
-            torch.cuda.synchronize()
-            return round(nbytes * reps / (e0.elapsed_time(e1) * 1e9), 3)
-
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        copy_tb = rate(lambda: dst.copy_(src), 4, 2 << 30)
-        x = src.view(torch.float64)
-        y = dst.view(torch.float64)
-        x.sum()
-        read_tb = rate(lambda: x.sum(), 10, 1 << 30)
-        write_tb = rate(lambda: y.fill_(1.0), 10, 1 << 30)
-        print(json.dumps({"probe": "copy", "bytes_read": 1 << 30, "bytes_written": 1 << 30, "launches": 5,
-                          "copy_TB_s": copy_tb, "read_TB_s": read_tb, "write_TB_s": write_tb}))
+        probe_copy(torch)
         return
     import ggemm as G
 
     W = WORKLOADS[args.workload]
-    Gp, m, n, k = W["G"], W["m"], W["n"], W["k"]
+    shapes = shapes_of(args.workload)
+    Gp = len(shapes)
     dev = torch.device("cuda:0")
     seed = 20261201 + W["seed"]
-    lda, ldb, ldc = m, k, m
-    A = torch.empty((Gp, k, m), dtype=torch.float64, device=dev)   # per problem column-major m x k
-    B = torch.empty((Gp, n, k), dtype=torch.float64, device=dev)
-    Cm = torch.empty((Gp, n, m), dtype=torch.float64, device=dev)
-    lo_hi = (-1.0, 1.0) if args.workload == "large" else None
-    fill(torch, A, W["phi"], seed, 0, lo_hi)
-    fill(torch, B, W["phi"], seed + 1, 10, lo_hi)
-    fill(torch, Cm, 0.0, seed + 2, 20)
-    C0 = Cm.clone() if W["beta"] != 0.0 else None
+    # per problem column-major: A m x k (torch (k, m)), B k x n (torch (n, k)), C m x n (torch (n, m))
+    A, B, Cm = [], [], []
+    for g, (m, n, k, a, b, phi, lo_hi, bad) in enumerate(shapes):
+        A.append(torch.empty((k, m), dtype=torch.float64, device=dev))
+        B.append(torch.empty((n, k), dtype=torch.float64, device=dev))
+        Cm.append(torch.empty((n, m), dtype=torch.float64, device=dev))
+        fill(torch, A[g], phi, seed + 101 * g, 0, lo_hi, bad)
+        fill(torch, B[g], phi, seed + 101 * g + 1, 10, lo_hi, bad)
+        fill(torch, Cm[g], 0.0, seed + 101 * g + 2, 20)
+    C0 = [c.clone() for c in Cm] if any(s[4] != 0.0 for s in shapes) else None
     torch.cuda.synchronize()
 
     def problems(Cbuf):
-        return [G.Problem(m, n, k, A[g].data_ptr(), lda, B[g].data_ptr(), ldb, Cbuf[g].data_ptr(), ldc,
-                          W["alpha"], W["beta"]) for g in range(Gp)]
+        return G.problems_array([G.Problem(m, n, k, A[g].data_ptr(), m, B[g].data_ptr(), k, Cbuf[g].data_ptr(), m, a, b)
+                                 for g, (m, n, k, a, b, *_r) in enumerate(shapes)])
 
-    fixed_n = 14 if args.workload == "plumbing" else 0
-    cfg = G.Config(fixed_n, 1e-15, 1, G.REPAIR_ON)
-    path = G.PATH_EMU_GROUPED
-    flops = 2.0 * Gp * m * n * k
-    h = G.Handle(Gp, Gp * m * k, Gp * k * n, Gp * m * n)
-    probs = G.problems_array(problems(Cm))
+    cfg = G.Config(W.get("fixed_n", 0), 1e-15, 1, G.REPAIR_ON)
+    path = G.PATH_AUTO if W["path"] == "AUTO" else G.PATH_EMU_GROUPED
+    flops = sum(2.0 * m * n * k for (m, n, k, *_r) in shapes)
+    sizes = [sum(s[0] * s[2] for s in shapes), sum(s[2] * s[1] for s in shapes), sum(s[0] * s[1] for s in shapes)]
+    h = G.Handle(Gp, *sizes, min_k=W.get("min_k"))
+    probs = problems(Cm)
     st = G.Stats()
 
     def call():
@@ -170,17 +236,18 @@ def main():
 
     plan = None
     timed = call
+    Cm2 = None
     if W.get("graph"):
         # the call planned once (ggemm_make_plan: a hipGraph), then per step the output pointers are
         # updated -- alternating between two C buffers -- and the plan executed on the same stream
-        Cm2 = torch.empty_like(Cm)
+        Cm2 = [torch.empty_like(c) for c in Cm]
         err = C.c_int(0)
         plan = G.lib().ggemm_make_plan_ex(h.h, path, C.byref(cfg), probs, Gp, C.byref(err))
         if not plan:
             raise RuntimeError(f"ggemm_make_plan_ex failed: {err.value}")
         if G.lib().ggemm_plan_get_stats(plan, C.byref(st)):
             raise RuntimeError("ggemm_plan_get_stats failed")
-        ptrs = lambda T: (C.c_void_p * Gp)(*[T[g].data_ptr() for g in range(Gp)])
+        ptrs = lambda T: (C.c_void_p * Gp)(*[t.data_ptr() for t in T])
         PA, PB, PC = ptrs(A), ptrs(B), (ptrs(Cm), ptrs(Cm2))
         step = [0]
 
@@ -192,11 +259,7 @@ def main():
                 raise RuntimeError(f"plan update / execute rc={rc}")
             step[0] += 1
 
-    def reset_c():
-        if C0 is not None:
-            Cm.copy_(C0)
-
-    # ---- timed region: K back-to-back calls (beta != 0 makes C drift; values are not checked here)
+    # ---- timed region: K back-to-back runs (beta != 0 makes C drift; values are checked afterwards)
     for _ in range(args.warmup):
         timed()
     torch.cuda.synchronize()
@@ -209,9 +272,18 @@ def main():
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
     ms = e0.elapsed_time(e1) / args.steps
-    N = st.moduli_max
-    planes = N + 1
-    int8_ops = planes * 2.0 * Gp * m * n * kp_of(k)
+    Nmax = st.moduli_max
+    # INT8 operations of the emulated problems: (N + 1) planes x 2 m n Kp each
+    plan_e = None
+    arr_plan = (G.PlanEntry * Gp)()
+    dm = G.DeviceModel()
+    props = torch.cuda.get_device_properties(0)
+    G.lib().ggemm_device_model_init(C.byref(dm), props.gcnArchName.encode(), 9, 5, props.multi_processor_count)
+    G.lib().ggemm_plan(probs, Gp, C.byref(cfg), path, C.byref(dm), arr_plan)
+    plan_e = list(arr_plan)
+    emu = [g for g in range(Gp) if plan_e[g].route == 0]
+    int8_ops = sum((plan_e[g].num_moduli + 1) * 2.0 * shapes[g][0] * shapes[g][1] * kp_of(shapes[g][2]) for g in emu)
+    emu_flops = sum(2.0 * shapes[g][0] * shapes[g][1] * shapes[g][2] for g in emu)
 
     # ---- per-stage kernel durations (HIP events around each launch on the handle's stream)
     G.lib().ggemm_profile_enable(1)
@@ -227,87 +299,53 @@ def main():
     st_ms = [stage[q] / max(ncalls.value, 1) for q in range(4)]
     i8_ms = st_ms[1]
     achieved = int8_ops / (i8_ms * 1e-3) / 1e12 if i8_ms > 0 else 0.0
-    prep_bytes = Gp * (8.0 * (m * k + n * k) + planes * (m + n) * kp_of(k) + 16.0 * (m + n))
+    prep_bytes = sum(8.0 * (shapes[g][0] * shapes[g][2] + shapes[g][1] * shapes[g][2]) +
+                     (plan_e[g].num_moduli + 1) * (shapes[g][0] + shapes[g][1]) * kp_of(shapes[g][2]) +
+                     16.0 * (shapes[g][0] + shapes[g][1]) for g in emu)
     # reconstruct: N digit bytes + the int32 abs-plane product per entry, C0 (beta != 0), C, shifts
-    recon_bytes = Gp * ((N + 4.0) * m * n + 8.0 * m * n * (2 if W["beta"] != 0 else 1) + 16.0 * (m + n))
+    recon_bytes = sum((plan_e[g].num_moduli + 4.0) * shapes[g][0] * shapes[g][1] +
+                      8.0 * shapes[g][0] * shapes[g][1] * (2 if shapes[g][4] != 0 else 1) +
+                      16.0 * (shapes[g][0] + shapes[g][1]) for g in emu)
 
+    # ---- validation of the timed configuration's own output
+    validation = None
+    if not args.no_validate:
+        validation, keep = validate_sampled(G, torch, shapes, A, B, C0, Cm, h, plan, path, cfg, plan_e, problems)
     if plan is not None:
         G.lib().ggemm_destroy_plan(plan)
+        plan_used = True
+    else:
+        plan_used = False
+    h.close()
+    if Cm2 is not None:
         del Cm2
-    h.close()   # free the timing workspace before the validation handle allocates its own
-
-    # ---- validation call with device counters on (separate handle; syncs per call)
-    os.environ["GGEMM_STATS_REPAIR"] = "1"
-    hv = G.Handle(Gp, Gp * m * k, Gp * k * n, Gp * m * n)
-    del os.environ["GGEMM_STATS_REPAIR"]
-    reset_c()
-    torch.cuda.synchronize()
-    stv = G.Stats()
-    rc = G.lib().ggemm_grouped_dgemm(hv.h, path, C.byref(cfg), probs, Gp, C.byref(stv))
-    torch.cuda.synchronize()
-    assert rc == 0
-    # sampled componentwise error vs an 80-bit host reference
-    rng = np.random.default_rng(7)
-    ns = 256 if args.workload != "large" else 64
-    worst_gamma = worst_norm = 0.0
-    u = 2.0 ** -53
-    nt = k + (W["alpha"] != 1.0) + (W["beta"] != 0.0)
-    gam = nt * u / (1 - nt * u)
-    for g in range(Gp):
-        ii = rng.integers(0, m, ns)
-        jj = rng.integers(0, n, ns)
-        a = A[g][:, torch.from_numpy(ii).to(dev)].cpu().numpy().T.astype(np.longdouble)   # ns x k
-        b = B[g][torch.from_numpy(jj).to(dev), :].cpu().numpy().astype(np.longdouble)     # ns x k
-        ref = W["alpha"] * (a * b).sum(axis=1)
-        den = abs(W["alpha"]) * np.abs(a * b).sum(axis=1)
-        if C0 is not None:
-            c0 = C0[g][torch.from_numpy(jj).to(dev), torch.from_numpy(ii).to(dev)].cpu().numpy().astype(np.longdouble)
-            ref = ref + W["beta"] * c0
-            den = den + abs(W["beta"]) * np.abs(c0)
-        got = Cm[g][torch.from_numpy(jj).to(dev), torch.from_numpy(ii).to(dev)].cpu().numpy().astype(np.longdouble)
-        err = np.abs(got - ref)
-        worst_gamma = max(worst_gamma, float(np.max(err / (gam * den))))
-        nrm = np.sqrt((a * a).sum(axis=1) * (b * b).sum(axis=1))
-        worst_norm = max(worst_norm, float(np.max(err / (abs(W["alpha"]) * nrm))))
+        torch.cuda.empty_cache()
+    if not args.no_validate:
+        validation.update(validate_counters(G, torch, shapes, C0, Cm, keep, path, cfg, problems, W.get("min_k")))
+        del keep
+        torch.cuda.empty_cache()
 
     # ---- native FP64 MFMA path on the same workload (context: the emulation must beat this)
     native_tflops = None
     if not args.no_native:
+        hn = G.Handle(Gp, *sizes, min_k=W.get("min_k"))
         cfgn = G.Config(0, 1e-15, 1, 0)
         for _ in range(2):
-            G.lib().ggemm_grouped_dgemm(hv.h, G.PATH_NATIVE_GROUPED, C.byref(cfgn), probs, Gp, None)
+            G.lib().ggemm_grouped_dgemm(hn.h, G.PATH_NATIVE_GROUPED, C.byref(cfgn), probs, Gp, None)
         torch.cuda.synchronize()
         reps = max(2, min(args.steps, 10))
         e0.record()
         for _ in range(reps):
-            G.lib().ggemm_grouped_dgemm(hv.h, G.PATH_NATIVE_GROUPED, C.byref(cfgn), probs, Gp, None)
+            G.lib().ggemm_grouped_dgemm(hn.h, G.PATH_NATIVE_GROUPED, C.byref(cfgn), probs, Gp, None)
         e1.record()
         torch.cuda.synchronize()
         native_tflops = flops / (e0.elapsed_time(e1) / reps * 1e-3) / 1e12
-    hv.close()
+        hn.close()
 
     # ---- CPU baseline: the host FP64 GEMM (OpenMP) on a bounded sample of the same problems
     cpu = None
     if not args.no_cpu_baseline:
-        sys.path.insert(0, str(REPO / "tests"))
-        import oracle_lib as O
-        ora = O.oracle()
-        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-        done, t_cpu, budget = 0, 0.0, 15.0
-        for g in range(Gp):
-            ha = A[g].cpu().numpy().reshape(-1)
-            hb = B[g].cpu().numpy().reshape(-1)
-            hc = np.zeros(m * n)
-            t1 = time.perf_counter()
-            ora.oz2o_dgemm(m, n, k, W["alpha"], ha, lda, hb, ldb, 0.0, hc, ldc)
-            t_cpu += time.perf_counter() - t1
-            done += 1
-            if t_cpu > budget or (args.workload == "large"):
-                break
-        cpu = {"value": round(2.0 * m * n * k * done / t_cpu / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
-               "kind": "port",
-               "sample": f"{done} of {Gp} problems ({m}x{n}x{k}) through the host blocked FP64 GEMM "
-                         f"(oracle/oz2_dgemm.c, OpenMP, {threads} threads), {t_cpu:.1f} s"}
+        cpu = cpu_baseline(shapes, A, B, budget_s=15.0)
 
     value = flops / (ms * 1e-3) / 1e12
     out = {
@@ -315,17 +353,15 @@ def main():
         "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms, 4), "wall_ms_per_step": round(wall_ms, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f64", "data": "synthetic",
-        "config": {"workload": W["desc"], "G": Gp, "m": m, "n": n, "k": k, "path": "EMU_GROUPED",
-                   "execution": "plan/execute (hipGraph), pointers updated per run" if plan is not None
+        "config": {"workload": W["desc"], "G": Gp, "shapes": summarize_shapes(shapes), "path": W["path"],
+                   "execution": "plan/execute (hipGraph), pointers updated per run" if plan_used
                    else "ggemm_grouped_dgemm per run",
-                   "num_moduli": N, "planes": planes, "repair": "ON"},
+                   "num_moduli": [st.moduli_min, st.moduli_max], "repair": "ON"},
         "int8_mfma_frac_end_to_end": round(int8_ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4),
         "fp64_mfma_frac": round(value / FP64_PEAK_TFLOPS, 4),
         "native_fp64_tflops": None if native_tflops is None else round(native_tflops, 3),
-        "max_err_over_gamma_sampled": worst_gamma, "max_normwise_rel_err_sampled": worst_norm,
-        "stats": {"num_fallback": stv.num_fallback, "num_repaired": stv.num_repaired,
-                  "num_uncertified": stv.num_uncertified, "num_safety_fallback": stv.num_safety_fallback,
-                  "kernel_launches": stv.kernel_launches, "moduli": [stv.moduli_min, stv.moduli_max]},
+        "emulated_flop_share": round(emu_flops / flops, 4),
+        "validation": validation,
         "stage_ms": {"prep": round(st_ms[0], 4), "int8_gemm": round(st_ms[1], 4), "reconstruct": round(st_ms[2], 4),
                      "native": round(st_ms[3], 4)},
         "stage_hbm_gbs": {"prep": round(prep_bytes / (st_ms[0] * 1e-3) / 1e9, 1) if st_ms[0] else None,
@@ -336,6 +372,130 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))
+
+
+def summarize_shapes(shapes):
+    seen = {}
+    for (m, n, k, *_r) in shapes:
+        seen[(m, n, k)] = seen.get((m, n, k), 0) + 1
+    if len(seen) > 4:
+        return f"{len(shapes)} ragged problems"
+    return [f"{c} x {m}x{n}x{k}" for (m, n, k), c in seen.items()]
+
+
+def validate_sampled(G, torch, shapes, A, B, C0, Cm, h, plan, path, cfg, plan_e, problems):
+    """The timed configuration's output, checked after the timed region: one more timed-style run
+    into Cm (for a plan: pointers updated to Cm, then executed); per problem 8 x 8 sampled entries
+    bitwise against the CPU oracle's emulation of those entries (emulated routes; each entry depends
+    only on its row of A, column of B and C0 entry) and against an 80-bit host dot (max err / gamma_n
+    and the normwise error, every route).  Returns the figures and a copy of the output."""
+    sys.path.insert(0, str(REPO / "tests"))
+    import oracle_lib as O
+    Gp = len(shapes)
+    if C0 is not None:
+        for g in range(Gp):
+            Cm[g].copy_(C0[g])
+    if plan is not None:
+        ptrs = lambda T: (C.c_void_p * Gp)(*[t.data_ptr() for t in T])
+        rc = G.lib().ggemm_plan_update_pointers(plan, ptrs(A), ptrs(B), ptrs(Cm))
+        rc = rc or G.lib().ggemm_execute_plan(plan, None)
+        if rc:
+            raise RuntimeError(f"plan update / execute rc={rc}")
+    else:
+        st = G.Stats()
+        rc = G.lib().ggemm_grouped_dgemm(h.h, path, C.byref(cfg), problems(Cm), Gp, C.byref(st))
+        if rc:
+            raise RuntimeError(f"ggemm_grouped_dgemm rc={rc}")
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(7)
+    worst_gamma = worst_norm = 0.0
+    sampled = mismatched = 0
+    u = 2.0 ** -53
+    for g, (m, n, k, a, b, *_r) in enumerate(shapes):
+        if a == 0.0:
+            continue
+        I = np.sort(rng.choice(m, min(8, m), replace=False))
+        J = np.sort(rng.choice(n, min(8, n), replace=False))
+        ii, jj = torch.as_tensor(I, device="cuda"), torch.as_tensor(J, device="cuda")
+        got = Cm[g][jj][:, ii].cpu().numpy()                       # |J| x |I|
+        av = np.ascontiguousarray(A[g][:, ii].cpu().numpy())       # k x |I|
+        bv = np.ascontiguousarray(B[g][jj].cpu().numpy())          # |J| x k
+        c0 = np.ascontiguousarray(C0[g][jj][:, ii].cpu().numpy()) if C0 is not None else np.zeros((len(J), len(I)))
+        if plan_e[g].route == 0:
+            want = c0.copy()
+            cnt = np.zeros(4, dtype=np.int64)
+            rc = O.oracle().oz2o_emulate(len(I), len(J), k, plan_e[g].num_moduli, av.reshape(-1), len(I),
+                                         bv.reshape(-1), k, want.reshape(-1), len(I), a, b, O.REPAIR_ON, cnt)
+            assert rc == 0
+            same = (want.view(np.int64) == got.view(np.int64)) | (np.isnan(want) & np.isnan(got))
+            sampled += same.size
+            mismatched += int((~same).sum())
+        fin = np.isfinite(got) & np.isfinite(av).all(axis=0)[None, :] & np.isfinite(bv).all(axis=1)[:, None]
+        if not fin.any():
+            continue
+        al, bl, cl = av.astype(np.longdouble), bv.astype(np.longdouble), c0.astype(np.longdouble)
+        ref = a * (bl @ al) + b * cl
+        den = abs(a) * (np.abs(bl) @ np.abs(al)) + abs(b) * np.abs(cl)
+        nt = k + (a != 1.0) + (b != 0.0)
+        gam = nt * u / (1 - nt * u)
+        err = np.abs(got.astype(np.longdouble) - ref)
+        worst_gamma = max(worst_gamma, float(np.max((err / (gam * den))[fin])))
+        nrm = np.sqrt(np.outer((bl * bl).sum(axis=1), (al * al).sum(axis=0)))
+        worst_norm = max(worst_norm, float(np.max((err / (abs(a) * nrm))[fin])))
+    keep = [c.clone() for c in Cm]
+    return ({"oracle_sampled_entries": sampled, "oracle_mismatches": mismatched,
+             "max_err_over_gamma_sampled": worst_gamma, "max_normwise_rel_err_sampled": worst_norm}, keep)
+
+
+def validate_counters(G, torch, shapes, C0, Cm, keep, path, cfg, problems, min_k):
+    """A direct ggemm_grouped_dgemm on a handle that reports the device counters: its output must
+    equal the timed configuration's output (keep) on every entry; its stats are reported."""
+    Gp = len(shapes)
+    if C0 is not None:
+        for g in range(Gp):
+            Cm[g].copy_(C0[g])
+    os.environ["GGEMM_STATS_REPAIR"] = "1"
+    hv = G.Handle(Gp, sum(s[0] * s[2] for s in shapes), sum(s[2] * s[1] for s in shapes),
+                  sum(s[0] * s[1] for s in shapes), min_k=min_k)
+    del os.environ["GGEMM_STATS_REPAIR"]
+    stv = G.Stats()
+    rc = G.lib().ggemm_grouped_dgemm(hv.h, path, C.byref(cfg), problems(Cm), Gp, C.byref(stv))
+    torch.cuda.synchronize()
+    hv.close()
+    if rc:
+        raise RuntimeError(f"validation call rc={rc}")
+    equal = all(bool(((x.view(torch.int64) == y.view(torch.int64)) | (torch.isnan(x) & torch.isnan(y))).all())
+                for x, y in zip(keep, Cm))
+    return {"direct_call_equals_timed_output": equal,
+            "stats": {"num_fallback": stv.num_fallback, "num_repaired": stv.num_repaired,
+                      "num_uncertified": stv.num_uncertified, "num_safety_fallback": stv.num_safety_fallback,
+                      "kernel_launches": stv.kernel_launches, "moduli": [stv.moduli_min, stv.moduli_max]}}
+
+
+def cpu_baseline(shapes, A, B, budget_s):
+    """The host blocked FP64 GEMM (oracle/oz2_dgemm.c, OpenMP) on as many of the workload's problems
+    as fit in about budget_s seconds (at least one), in the workload's order."""
+    sys.path.insert(0, str(REPO / "tests"))
+    import oracle_lib as O
+    ora = O.oracle()
+    model, mask, ncpu, naff = host_cpu()
+    threads = int(os.environ.get("OMP_NUM_THREADS", naff))
+    done, t_cpu, fl = 0, 0.0, 0.0
+    for g, (m, n, k, a, *_r) in enumerate(shapes):
+        ha = A[g].cpu().numpy().reshape(-1)
+        hb = B[g].cpu().numpy().reshape(-1)
+        hc = np.zeros(m * n)
+        t1 = time.perf_counter()
+        ora.oz2o_dgemm(m, n, k, 1.0, ha, m, hb, k, 0.0, hc, m)
+        t_cpu += time.perf_counter() - t1
+        fl += 2.0 * m * n * k
+        done += 1
+        if t_cpu > budget_s or (t_cpu > 0 and t_cpu / done * (done + 1) > 2 * budget_s):
+            break
+    return {"value": round(fl / t_cpu / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "cpu_model": model, "affinity": mask, "nproc": ncpu, "affinity_cpus": naff,
+            "sample": f"{done} of {len(shapes)} problems of the workload through the host blocked FP64 GEMM "
+                      f"(oracle/oz2_dgemm.c, OpenMP, {threads} threads), {t_cpu:.1f} s"}
 
 
 if __name__ == "__main__":

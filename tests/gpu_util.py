@@ -174,3 +174,37 @@ class WhiteboxRun:
 
     def C(self, g):
         return host(self.dC[g])
+
+
+def oracle_block(A_t, B_t, C0_t, k, alpha, beta, N, mode, I, J):
+    """The oracle's emulated values of the entries (I x J) of one problem, and its counters
+    [nonfinite vectors, uncertified, repaired, safety] over those entries.
+
+    Every output entry (i, j) of the Ozaki-II pipeline depends only on row i of A, column j of B
+    and C0(i, j): the row shift, abs shift and norm bounds are per row, the column ones per column,
+    the CRT / certificate / repair per entry.  So the sub-problem made of rows I of A, columns J of B
+    and C0(I, J) gives the oracle's exact bits for those entries at O(N k |I| |J|) cost.
+    Torch layouts (column-major with leading dimension = the last axis): A_t (k, >= m),
+    B_t (n, >= k), C0_t (n, >= m) or None when beta == 0.  Returns ((|J|, |I|) array, counters)."""
+    t = torch()
+    ii = t.as_tensor(np.asarray(I), device=A_t.device)
+    jj = t.as_tensor(np.asarray(J), device=A_t.device)
+    a = np.ascontiguousarray(A_t[:k][:, ii].cpu().numpy())          # (k, |I|): column-major |I| x k
+    b = np.ascontiguousarray(B_t[jj][:, :k].cpu().numpy())          # (|J|, k): column-major k x |J|
+    if C0_t is None or beta == 0.0:
+        c = np.zeros((len(J), len(I)))
+    else:
+        c = np.ascontiguousarray(C0_t[jj][:, ii].cpu().numpy())     # (|J|, |I|): column-major |I| x |J|
+    cnt = np.zeros(4, dtype=np.int64)
+    rc = O.oracle().oz2o_emulate(len(I), len(J), k, N, a.reshape(-1), len(I), b.reshape(-1), k, c.reshape(-1),
+                                 len(I), alpha, beta, mode, cnt)
+    assert rc == 0, rc
+    return c, cnt
+
+
+def gpu_block(C_t, I, J):
+    """Entries (I x J) of a device result in torch layout (n, >= m), as a (|J|, |I|) array."""
+    t = torch()
+    ii = t.as_tensor(np.asarray(I), device=C_t.device)
+    jj = t.as_tensor(np.asarray(J), device=C_t.device)
+    return C_t[jj][:, ii].cpu().numpy()

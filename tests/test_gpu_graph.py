@@ -8,8 +8,9 @@ import pytest
 import torch
 
 import ggemm as G
+import oracle_lib as O
 from gpu_util import host, same_bits, say
-from test_gpu_grouped import CFG_AUTO, Case
+from test_gpu_grouped import CFG_AUTO, Case, oracle_plan
 
 pytestmark = pytest.mark.gpu
 
@@ -117,3 +118,38 @@ def test_plan_rejects_other_paths_and_bad_pointers():
     assert G.lib().ggemm_plan_update_pointers(plan, None, None, null) == G.GGEMM_ERR_INVALID
     G.lib().ggemm_destroy_plan(plan)
     h.close()
+
+
+def test_plan_update_pointers_long_k_matches_oracle():
+    """A plan whose calls take the long-k production layout (row-major residues, blocked digits;
+    largest Kp > 4096), executed on data set X, re-pointed to Y (ggemm_plan_update_pointers) and
+    executed again: both outputs bitwise equal to the oracle's in COUNT mode."""
+    shapes = [(256, 256, 4160)] * 2 + [(128, 96, 16384)]
+    X = Case(shapes, 61, phi=1.0, beta=0.5)
+    Y = Case(shapes, 62, phi=1.0, beta=0.5)
+    cfg = G.Config(0, 1e-15, 0, G.REPAIR_COUNT)
+    rc, plan_o = oracle_plan(X, cfg, G.PATH_EMU_GROUPED)
+    assert rc == 0
+    h = G.Handle(len(shapes), *[max(a, b) for a, b in zip(X.sizes(), Y.sizes())])
+    X.reset_C()
+    Y.reset_C()
+    arr = G.problems_array(X.problems())
+    err = C.c_int(0)
+    plan = G.lib().ggemm_make_plan_ex(h.h, G.PATH_EMU_GROUPED, C.byref(cfg), arr, len(shapes), C.byref(err))
+    assert plan, err.value
+    try:
+        say("long-k plan on X")
+        assert G.lib().ggemm_execute_plan(plan, None) == 0
+        torch.cuda.synchronize()
+        ptr = lambda ts: (C.c_void_p * len(shapes))(*[t.data_ptr() for t in ts])
+        assert G.lib().ggemm_plan_update_pointers(plan, ptr(Y.dA), ptr(Y.dB), ptr(Y.dC)) == 0
+        say("long-k plan re-pointed to Y")
+        assert G.lib().ggemm_execute_plan(plan, None) == 0
+        torch.cuda.synchronize()
+        for case in (X, Y):
+            for g, (hp, e) in enumerate(zip(case.hp, plan_o)):
+                Co, _ = hp.emulate(O.REPAIR_COUNT, e.num_moduli)
+                assert same_bits(case.C(g), Co), f"problem {g} differs"
+    finally:
+        G.lib().ggemm_destroy_plan(plan)
+        h.close()

@@ -282,6 +282,27 @@ def test_default_kernel_choice():
         assert same_bits(a, b)
 
 
+def test_default_layout_long_k_matches_oracle():
+    """The production layout of every call whose largest Kp exceeds 4096 -- row-major residue
+    planes, 16 x 16 blocked digits -- bitwise against the oracle in COUNT mode (uncertified entries
+    keep their emulated values), on the default handle (general INT8 kernel for this small group)
+    and with the 256 x 256 kernel forced; mixed N (15 at k = 4160, 16 at k = 16384)."""
+    case = Case([(256, 256, 4160)] * 3 + [(128, 96, 16384)], 20261230, phi=1.0, beta=0.5)
+    cfg = G.Config(0, 1e-15, 0, G.REPAIR_COUNT)
+    rc, plan = oracle_plan(case, cfg, G.PATH_EMU_GROUPED)
+    assert rc == 0 and [e.num_moduli for e in plan] == [15, 15, 15, 16]
+    want = [h.emulate(O.REPAIR_COUNT, e.num_moduli) for h, e in zip(case.hp, plan)]
+    for kernel, name in ((None, "i8_grouped_kernel"), ("large", "i8_large_kernel")):
+        say(f"long-k default layout, kernel {name}")
+        with kernel_handle(case, kernel) as h:
+            rc, st = run(case, G.PATH_EMU_GROUPED, cfg, handle=h)
+            assert rc == 0 and G.lib().ggemm_profile_i8_kernel().decode() == name
+        assert (st.moduli_min, st.moduli_max, st.kernel_launches) == (15, 16, 3)
+        for g, (Co, cnt) in enumerate(want):
+            assert same_bits(case.C(g), Co), f"{name}: problem {g} differs"
+        assert st.num_uncertified == sum(int(c[1]) for _, c in want)
+
+
 @pytest.mark.parametrize("shapes", [[(300, 270, 200)] * 2 + [(17, 33, 90), (64, 48, 40)],   # general kernel
                                     [(520, 600, 470)] * 3],                                   # large-tile kernel
                          ids=["general", "large"])
@@ -392,7 +413,10 @@ def test_native_tile_sizes_bitwise(path, beta):
     same ragged group -- partial tiles on both edges, k not a multiple of the 16-deep stage, k = 0
     and empty problems: every output bit equal (each entry takes the same k-ordered MFMA chain at
     either size), each problem within the gamma_n gate of the host reference."""
-    shapes = [(300, 200, 77), (128, 128, 16), (129, 257, 300), (1, 1, 1), (33, 17, 0), (0, 5, 5), (260, 140, 1)]
+    shapes = [(300, 200, 77), (128, 128, 16), (129, 257, 300), (1, 1, 1), (33, 17, 0), (0, 5, 5), (260, 140, 1),
+              # full tiles of both sizes over several 16-deep stages (the bounds-test-free path), next
+              # to partial tiles of the same problem
+              (256, 256, 64), (384, 256, 1024), (260, 128, 48)]
     outs = {}
     for tile in ("64", "128"):
         case = Case(shapes, 33, phi=1.0, alpha=1.5, beta=beta)
