@@ -34,6 +34,9 @@ struct GroupedCall {
 };
 
 int validate(ggemm_handle_t h, const ggemm_problem_t* p, int num);
+// Workspace sizes of a handle for the given capacity (src/ggemm.cu:228-341 rules): fills A8_bytes,
+// B8_bytes, C32_bytes, row_shift_elems, col_shift_elems and desc_bytes; allocates nothing.
+void size_workspace(ggemm_handle_s* h, int max_problems, size_t max_A, size_t max_B, size_t max_C, int min_k);
 int repair_mode_of(ggemm_path_t path, const ggemm_config_t* cfg);   // OZ2_REPAIR_* or -1
 int counters_reset(ggemm_handle_t h, hipStream_t s);
 int counters_read(ggemm_handle_t h, hipStream_t s, ggemm_stats_t* st);

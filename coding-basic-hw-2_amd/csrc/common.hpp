@@ -59,6 +59,8 @@ struct DevCtx {
   unsigned long long* counters;     // device, 4 entries
 };
 DevCtx* dev_ctx();                  // current device; nullptr on failure
+// Device addresses of the resident tables and counters on the current device (0 on success).
+int device_state(void** tables, void** counters);
 
 // Native FP64 problem descriptor (device-resident so a captured graph can be re-pointed).
 struct F64Problem {

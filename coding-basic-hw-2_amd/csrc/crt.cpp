@@ -157,7 +157,8 @@ int build(CrtTables* t) {
 }
 
 std::mutex g_ctx_mu;
-DevCtx* g_ctx[64] = {};
+DevCtx g_ctx_store[64];
+bool g_ctx_ready[64] = {};
 
 }  // namespace
 
@@ -167,32 +168,27 @@ const CrtTables* host_tables() {
   return st == 0 ? &tab : nullptr;
 }
 
+// The tables and counters are device globals (device_state); the first use on a device copies the
+// host-built tables there (a plain copy: nothing is allocated on the device).
 DevCtx* dev_ctx() {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
   std::lock_guard<std::mutex> lk(g_ctx_mu);
-  if (g_ctx[dev]) return g_ctx[dev];
+  DevCtx* c = &g_ctx_store[dev];
+  if (g_ctx_ready[dev]) return c;
   const CrtTables* h = host_tables();
   if (!h) return nullptr;
-  DevCtx* c = new DevCtx{};
   c->device = dev;
   if (hipDeviceGetAttribute(&c->num_cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
       c->num_cus <= 0)
     c->num_cus = 256;
   void* tab = nullptr;
   void* cnt = nullptr;
-  if (hipMalloc(&tab, sizeof(CrtTables)) != hipSuccess ||
-      hipMalloc(&cnt, 4 * sizeof(unsigned long long)) != hipSuccess ||
-      hipMemcpy(tab, h, sizeof(CrtTables), hipMemcpyHostToDevice) != hipSuccess ||
-      hipMemset(cnt, 0, 4 * sizeof(unsigned long long)) != hipSuccess) {
-    if (tab) (void)hipFree(tab);
-    if (cnt) (void)hipFree(cnt);
-    delete c;
+  if (device_state(&tab, &cnt) != 0 || hipMemcpy(tab, h, sizeof(CrtTables), hipMemcpyHostToDevice) != hipSuccess)
     return nullptr;
-  }
   c->tab = static_cast<const CrtTables*>(tab);
   c->counters = static_cast<unsigned long long*>(cnt);
-  g_ctx[dev] = c;
+  g_ctx_ready[dev] = true;
   return c;
 }
 

@@ -392,6 +392,32 @@ double kp_inflation(int min_k) {
   return f;
 }
 
+}  // namespace
+
+// src/ggemm.cu:228-341 sizing rules (see ggemm_create_ex)
+void ggemm::size_workspace(ggemm_handle_s* h, int max_problems, size_t max_A, size_t max_B, size_t max_C, int min_k) {
+  const size_t P = (size_t)max_problems;
+  const size_t M = (size_t)kMaxPlanes;
+  const double infl = std::max(2.0, kp_inflation(min_k));
+  const size_t planeA = (size_t)std::ceil(infl * (double)max_A) + P * kBufAlign;
+  const size_t planeB = (size_t)std::ceil(infl * (double)max_B) + P * kBufAlign;
+  h->A8_bytes = M * planeA;
+  h->B8_bytes = M * planeB;
+  h->C32_bytes = M * (max_C + P * (kBufAlign / 4)) * sizeof(int32_t);
+  const size_t rowsA = std::min(max_A, M * planeA / (3 * kKpAlign));
+  const size_t colsB = std::min(max_B, M * planeB / (3 * kKpAlign));
+  h->row_shift_elems = OZ2_ROW_WS_PER_ROW * rowsA + P * 64;
+  h->col_shift_elems = OZ2_ROW_WS_PER_ROW * colsB + P * 64;
+  // descriptor blob: worst case over the paths (grouped, per-plane and per-problem images)
+  const size_t n_i8 = P * M;
+  const size_t si8 = std::max({sched_img((int)n_i8), n_i8 * sched_img(1), P * sched_img(kMaxPlanes)});
+  const size_t sf64 = std::max(sched_img((int)P), P * sched_img(1));
+  const BlobLayout Lw = layout_for(P, 2 * P, n_i8, P, sf64, sched_img((int)n_i8));
+  h->desc_bytes = align_up(Lw.total + si8 + kBufAlign, kBufAlign);
+}
+
+namespace {
+
 // Native problems idx[0..cnt): one grouped FP64 launch, or one launch per problem (loop).
 int run_native(ggemm_handle_t h, const ggemm_problem_t* probs, const int* idx, int cnt, bool grouped, int* launches) {
   if (cnt == 0) return GGEMM_OK;
@@ -639,28 +665,12 @@ extern "C" int ggemm_create_ex(ggemm_handle_t* out, int max_problems, size_t max
   ggemm_device_model_init(&h->dm, prop.gcnArchName, prop.major, prop.minor, h->num_cus);
   if (oz2_init_constants() != 0) FAIL(GGEMM_ERR_NUMERICS);
 
-  const double infl = std::max(2.0, kp_inflation(min_k));
-  const size_t planeA = (size_t)std::ceil(infl * (double)max_A) + P * kBufAlign;
-  const size_t planeB = (size_t)std::ceil(infl * (double)max_B) + P * kBufAlign;
-  h->A8_bytes = M * planeA;
-  h->B8_bytes = M * planeB;
-  h->C32_bytes = M * (max_C + P * (kBufAlign / 4)) * sizeof(int32_t);
-  const size_t rowsA = std::min(max_A, M * planeA / (3 * kKpAlign));
-  const size_t colsB = std::min(max_B, M * planeB / (3 * kKpAlign));
-  h->row_shift_elems = OZ2_ROW_WS_PER_ROW * rowsA + P * 64;
-  h->col_shift_elems = OZ2_ROW_WS_PER_ROW * colsB + P * 64;
+  size_workspace(h, max_problems, max_A, max_B, max_C, min_k);
   HIPA(hipMalloc(&h->A8, h->A8_bytes));
   HIPA(hipMalloc(&h->B8, h->B8_bytes));
   HIPA(hipMalloc(&h->C32, h->C32_bytes));
   HIPA(hipMalloc(&h->row_shift, h->row_shift_elems * sizeof(int32_t)));
   HIPA(hipMalloc(&h->col_shift, h->col_shift_elems * sizeof(int32_t)));
-
-  // descriptor blob: worst case over the paths (grouped, per-plane and per-problem images)
-  const size_t n_i8 = P * M;
-  const size_t si8 = std::max({sched_img((int)n_i8), n_i8 * sched_img(1), P * sched_img(kMaxPlanes)});
-  const size_t sf64 = std::max(sched_img((int)P), P * sched_img(1));
-  const BlobLayout Lw = layout_for(P, 2 * P, n_i8, P, sf64, sched_img((int)n_i8));
-  h->desc_bytes = align_up(Lw.total + si8 + kBufAlign, kBufAlign);
   HIPA(hipMalloc(&h->d_desc, h->desc_bytes));
   HIPA(hipHostMalloc(&h->h_desc, h->desc_bytes * kSlots, hipHostMallocDefault));
   for (int s = 0; s < kSlots; ++s) {

@@ -19,6 +19,9 @@ REPAIR_DEFAULT, REPAIR_OFF, REPAIR_COUNT, REPAIR_ON = 0, 1, 2, 3
 OZ2_REPAIR_OFF, OZ2_REPAIR_COUNT, OZ2_REPAIR_ON = 0, 1, 2
 MAX_MODULI = 20
 MAX_K_EXACT = 131040
+NOALLOC_SCRATCH_BYTES = 64 << 20
+NOALLOC_MAX_PROBLEMS = 64
+NOALLOC_MAX_ELEMS = 262144
 SHIFT_NONFINITE = -2147483648
 SHIFT_ZERO = -2147483647
 ROUTES = ["EMU", "EMPTY", "K_ZERO", "K_TOO_LARGE", "TINY", "UNPROFITABLE", "PRECISION", "SMALL_K", "ALPHA_ZERO"]
@@ -109,6 +112,8 @@ SIGNATURES = [
     ("ggemm_destroy", None, [_P]),
     ("ggemm_grouped_dgemm", C.c_int, [_P, C.c_int, C.POINTER(Config), C.POINTER(Problem), C.c_int,
                                       C.POINTER(Stats)]),
+    ("ggemm_grouped_dgemm_noalloc", C.c_int, [C.c_int, C.POINTER(Config), C.POINTER(Problem), C.c_int, _P,
+                                              C.POINTER(Stats)]),
     ("ggemm_make_plan", _P, [_P, C.c_int, C.POINTER(Config), C.POINTER(Problem), C.c_int]),
     ("ggemm_make_plan_ex", _P, [_P, C.c_int, C.POINTER(Config), C.POINTER(Problem), C.c_int, C.POINTER(C.c_int)]),
     ("ggemm_execute_plan", C.c_int, [_P, _P]),

@@ -104,6 +104,25 @@ void ggemm_destroy(ggemm_handle_t h);
 int ggemm_grouped_dgemm(ggemm_handle_t h, ggemm_path_t path, const ggemm_config_t* cfg,
                         const ggemm_problem_t* problems, int num_problems, ggemm_stats_t* stats);
 
+/* No counterpart in the reference.  ggemm_grouped_dgemm without a handle and without allocating
+ * anything, for callers that cannot allocate device memory (code under stream capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Same kernels, layouts and results (bit for bit) as a call
+ * through a handle created with ggemm_create(GGEMM_NOALLOC_MAX_PROBLEMS, GGEMM_NOALLOC_MAX_ELEMS x 3):
+ * the workspace is a static device array of GGEMM_NOALLOC_SCRATCH_BYTES that each GPU the library
+ * runs on holds until the process ends.  Paths GGEMM_PATH_EMU_GROUPED and GGEMM_PATH_AUTO only
+ * (others: GGEMM_ERR_INVALID).  Limits: at most GGEMM_NOALLOC_MAX_PROBLEMS problems
+ * (GGEMM_ERR_INVALID) and sum m*k, sum k*n, sum m*n each at most GGEMM_NOALLOC_MAX_ELEMS, residues
+ * counted at Kp = round_up(k, 32) (GGEMM_ERR_WORKSPACE); either error prints one line on stderr.
+ * Work runs on `stream`; the call returns after its descriptor copy has landed, i.e. after earlier
+ * work on the stream.  Every call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * from different streams race.  Device counters and GGEMM_STATS_REPAIR as for ggemm_grouped_dgemm. */
+#define GGEMM_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+#define GGEMM_NOALLOC_MAX_PROBLEMS 64
+#define GGEMM_NOALLOC_MAX_ELEMS ((size_t)262144)
+int ggemm_grouped_dgemm_noalloc(ggemm_path_t path, const ggemm_config_t* cfg,
+                                const ggemm_problem_t* problems, int num_problems, hipStream_t stream,
+                                ggemm_stats_t* stats);
+
 #ifdef __cplusplus
 }
 static_assert(sizeof(ggemm_problem_t) == 80, "ggemm_problem_t layout");
