@@ -206,15 +206,23 @@ def main():
     dev = torch.device("cuda:0")
     seed = 20261201 + W["seed"]
     # per problem column-major: A m x k (torch (k, m)), B k x n (torch (n, k)), C m x n (torch (n, m))
-    A, B, Cm = [], [], []
-    for g, (m, n, k, a, b, phi, lo_hi, bad) in enumerate(shapes):
-        A.append(torch.empty((k, m), dtype=torch.float64, device=dev))
-        B.append(torch.empty((n, k), dtype=torch.float64, device=dev))
-        Cm.append(torch.empty((n, m), dtype=torch.float64, device=dev))
-        fill(torch, A[g], phi, seed + 101 * g, 0, lo_hi, bad)
-        fill(torch, B[g], phi, seed + 101 * g + 1, 10, lo_hi, bad)
-        fill(torch, Cm[g], 0.0, seed + 101 * g + 2, 20)
-    C0 = [c.clone() for c in Cm] if any(s[4] != 0.0 for s in shapes) else None
+    # one flat buffer per operand, filled by one generator call (every problem of a workload shares
+    # phi, range and non-finite rate); problem g is a 256-byte aligned view
+    phi, lo_hi, bad = shapes[0][5:8]
+
+    def operand(dims, salt, phi_, lo_hi_, bad_):
+        offs, tot = [], 0
+        for d in dims:
+            offs.append(tot)
+            tot += (d[0] * d[1] + 31) // 32 * 32
+        flat = torch.empty(max(tot, 1), dtype=torch.float64, device=dev)
+        fill(torch, flat, phi_, seed + salt, salt, lo_hi_, bad_)
+        return [flat[o:o + d[0] * d[1]].view(d[0], d[1]) for o, d in zip(offs, dims)]
+
+    A = operand([(k, m) for (m, n, k, *_r) in shapes], 0, phi, lo_hi, bad)
+    B = operand([(n, k) for (m, n, k, *_r) in shapes], 10, phi, lo_hi, bad)
+    Cm = operand([(n, m) for (m, n, k, *_r) in shapes], 20, 0.0, None, 0.0)
+    C0 = [c.clone() for c in Cm] if any(x[4] != 0.0 for x in shapes) else None
     torch.cuda.synchronize()
 
     def problems(Cbuf):

@@ -43,6 +43,7 @@
 #include <cmath>
 #include <cstring>
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 #include "common.hpp"
@@ -75,7 +76,7 @@ struct Cfg {
   static constexpr int VM = (PA + PB) / NW;            // DMA instructions per wave and stage
   static constexpr int SMEM = NST * STAGE;
   // k loop with the stage barrier between the two halves of a stage's MFMAs (below): pays for
-  // the 16-wave kernel (one workgroup per compute unit), not for the general kernel's two
+  // the large-tile kernels (one workgroup per compute unit), not for the general kernel's two
   // workgroups
   static constexpr bool kSplit = NW >= 16;
   static_assert((PA + PB) % NW == 0 && FM >= 1 && FN >= 1, "tile split");
@@ -96,6 +97,16 @@ constexpr int kThreadsL = CfgL::NT;
 constexpr int kSmemL = CfgL::SMEM;
 
 __device__ __forceinline__ int swz(int row, int ch) { return ch ^ ((row >> 1) & 3); }
+
+// f(integral_constant<int, I>) for I = B .. E - 1: indices of accumulator arrays stay compile-time
+// constants (a loop the unroller declines to flatten would put the accumulators in memory)
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
 
 // ds_read_b128 at LDS byte address addr + OFF
 template <int OFF>
@@ -218,12 +229,10 @@ __device__ __forceinline__ void store_blocked(const v4i (&acc)[C::FM][C::FN], co
                                               int kind, int bi0, int bj0, int mb, int lane) {
   GLOBAL uint8_t* const y8 = ((GLOBAL uint8_t*)P.C) + 4 * lane;
   GLOBAL int32_t* const y32 = ((GLOBAL int32_t*)P.C) + 4 * lane;
-#pragma unroll
-  for (int j = 0; j < C::FN; ++j)
-#pragma unroll
-    for (int i = 0; i < C::FM; ++i) {
-      const int bi = bi0 + i, bj = bj0 + j;
-      if (bi * 16 >= P.m || bj * 16 >= P.n) continue;   // wave-uniform
+  static_for<0, C::FN * C::FM>([&](auto ij) {
+    constexpr int j = decltype(ij)::value / C::FM, i = decltype(ij)::value % C::FM;
+    const int bi = bi0 + i, bj = bj0 + j;
+    if (bi * 16 < P.m && bj * 16 < P.n) {   // wave-uniform
       const size_t e0 = ((size_t)bj * mb + bi) * 256;
       const v4i v = acc[i][j];
       if (kind == 0) {
@@ -242,6 +251,61 @@ __device__ __forceinline__ void store_blocked(const v4i (&acc)[C::FM][C::FN], co
         *reinterpret_cast<GLOBAL uint32_t*>(y8 + e0) = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
       }
     }
+  });
+}
+
+// Epilogue of a tile: the accumulators of the wave (wm, wn) = (wave % WGM, wave / WGM) stored as int32
+// or residue bytes, blocked or column-major (I8Epi).
+template <class C>
+__device__ __forceinline__ void tile_epilogue(const v4i (&acc)[C::FM][C::FN], const i8_problem& P, const I8Epi& epi,
+                                              int row0, int col0, int wave, int lane) {
+  constexpr int FM = C::FM, FN = C::FN;
+  const int wm = wave % C::WGM, wn = wave / C::WGM;
+  // D block layout: lane l, register r -> row 4 (l / 16) + r, column l % 16; a lane's 4 values
+  // are 4 consecutive rows of one column, i.e. contiguous in the column-major output, and the
+  // 64 lanes' values are one 16 x 16 block of the blocked output layout.
+  const bool residue = (epi.mode & kEpiResidue) != 0;
+  if (epi.mode & kEpiBlocked) {   // every existing block is stored whole (padding included)
+    // block (bi, bj) of the wave: uniform offset (bj MB + bi) 256 entries, lane l at entries 4 l
+    const int mb = (P.m + 15) / 16;
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    const int bi0 = (row0 + (wv % C::WGM) * C::WM) / 16, bj0 = (col0 + (wv / C::WGM) * C::WN) / 16;
+    const int kind = !residue ? 0 : (epi.mode & kEpiAccBias) ? 1 : 2;
+    store_blocked<C>(acc, P, epi, kind, bi0, bj0, mb, lane);
+    return;
+  }
+  const size_t ldc = (size_t)P.m;
+  const bool vec = (P.m % 4 == 0) && ((reinterpret_cast<uintptr_t>(P.C) & (residue ? 3 : 15)) == 0);
+  static_for<0, FM * FN>([&](auto ij) {
+    constexpr int i = decltype(ij)::value / FN, j = decltype(ij)::value % FN;
+    const int col = col0 + wn * C::WN + j * 16 + (lane & 15);
+    const int r0 = row0 + wm * C::WM + i * 16 + 4 * (lane >> 4);
+    if (col < P.n && r0 < P.m) {
+      const v4i v = acc[i][j];
+      if (!residue) {
+        GLOBAL int32_t* out = ((GLOBAL int32_t*)P.C) + (size_t)r0 + (size_t)col * ldc;
+        if (vec && r0 + 3 < P.m) {
+          *reinterpret_cast<GLOBAL v4i*>(out) = v;
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (r0 + r < P.m) out[r] = v[r];
+        }
+      } else {
+        GLOBAL uint8_t* out = ((GLOBAL uint8_t*)P.C) + (size_t)r0 + (size_t)col * ldc;
+        uint32_t y[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) y[r] = (epi.mode & kEpiAccBias) ? residue_byte<true>(v[r], epi) : residue_byte<false>(v[r], epi);
+        if (vec && r0 + 3 < P.m) {
+          *reinterpret_cast<GLOBAL uint32_t*>(out) = y[0] | (y[1] << 8) | (y[2] << 16) | (y[3] << 24);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (r0 + r < P.m) out[r] = (uint8_t)y[r];
+        }
+      }
+    }
+  });
 }
 
 template <class C, bool kPacked>
@@ -387,52 +451,7 @@ __device__ __forceinline__ void run_tile(uint8_t* lds, const i8_problem& P, cons
     }
   }
 
-  // D block layout: lane l, register r -> row 4 (l / 16) + r, column l % 16; a lane's 4 values
-  // are 4 consecutive rows of one column, i.e. contiguous in the column-major output, and the
-  // 64 lanes' values are one 16 x 16 block of the blocked output layout.
-  const bool residue = (epi.mode & kEpiResidue) != 0;
-  if (epi.mode & kEpiBlocked) {   // every existing block is stored whole (padding included)
-    // block (bi, bj) of the wave: uniform offset (bj MB + bi) 256 entries, lane l at entries 4 l
-    const int mb = (P.m + 15) / 16;
-    const int wv = __builtin_amdgcn_readfirstlane(wave);
-    const int bi0 = (row0 + (wv % C::WGM) * C::WM) / 16, bj0 = (col0 + (wv / C::WGM) * C::WN) / 16;
-    const int kind = !residue ? 0 : (epi.mode & kEpiAccBias) ? 1 : 2;
-    store_blocked<C>(acc, P, epi, kind, bi0, bj0, mb, lane);
-    return;
-  }
-  const size_t ldc = (size_t)P.m;
-  const bool vec = (P.m % 4 == 0) && ((reinterpret_cast<uintptr_t>(P.C) & (residue ? 3 : 15)) == 0);
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int col = col0 + wn * C::WN + j * 16 + (lane & 15);
-      const int r0 = row0 + wm * C::WM + i * 16 + 4 * (lane >> 4);
-      if (col >= P.n || r0 >= P.m) continue;
-      const v4i v = acc[i][j];
-      if (!residue) {
-        GLOBAL int32_t* out = ((GLOBAL int32_t*)P.C) + (size_t)r0 + (size_t)col * ldc;
-        if (vec && r0 + 3 < P.m) {
-          *reinterpret_cast<GLOBAL v4i*>(out) = v;
-        } else {
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            if (r0 + r < P.m) out[r] = v[r];
-        }
-      } else {
-        GLOBAL uint8_t* out = ((GLOBAL uint8_t*)P.C) + (size_t)r0 + (size_t)col * ldc;
-        uint32_t y[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) y[r] = (epi.mode & kEpiAccBias) ? residue_byte<true>(v[r], epi) : residue_byte<false>(v[r], epi);
-        if (vec && r0 + 3 < P.m) {
-          *reinterpret_cast<GLOBAL uint32_t*>(out) = y[0] | (y[1] << 8) | (y[2] << 16) | (y[3] << 24);
-        } else {
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            if (r0 + r < P.m) out[r] = (uint8_t)y[r];
-        }
-      }
-    }
+  tile_epilogue<C>(acc, P, epi, row0, col0, wave, lane);
 }
 
 // Tile of workgroup blockIdx.x: XCD-aware remap of the dispatch index (a permutation of
@@ -661,6 +680,7 @@ int i8_launch(const i8_problem* d_probs, const I8Epi* d_epi, const void* d_sched
   if (kernel == kI8Large)
     hipLaunchKernelGGL(i8_large_kernel, dim3((unsigned)info->tiles_main), dim3(kThreadsL), kSmemL, s, d_probs, d_epi,
                        static_cast<const int*>(d_sched));
+
   else
     hipLaunchKernelGGL(i8_grouped_kernel, dim3((unsigned)info->tiles_main), dim3(kThreads), kSmem, s, d_probs, d_epi,
                        static_cast<const int*>(d_sched));
