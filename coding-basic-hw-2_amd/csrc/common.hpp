@@ -74,8 +74,13 @@ struct F64Problem {
 // Schedule image shared by the tile-based kernels (INT8 GEMM, FP64 GEMM):
 //   int[0] total tiles, int[1] entries, int[2] tiles per entry when all entries have the same
 //   count (INT8 GEMM; 0 otherwise), int[3..7] reserved,
-//   prefix[entries + 1] (first tile of each entry), entry[entries] = (problem << 2) | cfg.
-constexpr int kSchedHdr = 8;
+//   INT8 GEMM only: int[kHdrXcd + x], x = 0..8, first tile of XCD x's queue (x = 8: the total);
+//   int[kHdrCtr + x], x < 8, the queue counters and int[kHdrDone] the finished-workgroup count
+//   of the persistent kernel (zero when uploaded, reset by the kernel itself),
+//   prefix[entries + 1] at kSchedHdr (first tile of each entry), entry[entries] = (problem << 2) | cfg.
+constexpr int kXcds = 8;   // MI355X: accelerator complex dies, each with its own L2
+constexpr int kHdrXcd = 8, kHdrCtr = 32, kHdrDone = 40;
+constexpr int kSchedHdr = 64;
 inline size_t sched_bytes(int entries) {
   return sizeof(int) * (size_t)(kSchedHdr + 2 * (size_t)entries + 1 + 8);
 }
@@ -125,15 +130,20 @@ __host__ __device__ inline size_t blocked_word(int r4, int c, int mb) {
   return ((size_t)(c >> 4) * (size_t)mb + (size_t)(r4 >> 4)) * 256 + (size_t)(16 * ((r4 & 15) >> 2) + (c & 15)) * 4;
 }
 // INT8 GEMM kernels: the general one (tile configs 0..2, two workgroups per compute unit) and the
-// large-tile one (every tile 256 x 256, one 16-wave workgroup per compute unit).
-enum { kI8General = 0, kI8Large = 1 };
+// large-tile one (every tile 256 x 256, one 16-wave workgroup per compute unit); kI8Persistent
+// added: their persistent work-stealing form instead of one workgroup per tile.
+enum { kI8General = 0, kI8Large = 1, kI8Persistent = 2 };
 // Builds the INT8 schedule (LPT order); cfg < 0 in a problem selects automatically.
 // large: kLargeNever, kLargeAuto (the large-tile kernel when every product is on automatic large
 // tiles and they fill the GPU) or kLargeForce (whenever every product's tile is automatic);
+// persistent: schedule for the persistent kernels (queues per XCD);
 // *kernel receives the choice, which i8_launch must be given.
 enum { kLargeNever = 0, kLargeAuto = 1, kLargeForce = 2 };
 int i8_build_schedule(const i8_problem* h, int num, void* h_ws, size_t ws_bytes, i8_sched_info* info,
-                      int num_cus, int large = kLargeNever, int* kernel = nullptr);
+                      int num_cus, int large = kLargeNever, int* kernel = nullptr, bool persistent = false);
+// GGEMM_I8_SCHED=persistent in the environment (read at each call): the kernel-level INT8 API
+// (i8_grouped_gemm_*) builds for and runs the persistent kernels
+bool i8_env_persistent();
 // d_epi: per-problem epilogues in device memory, or nullptr for int32 products everywhere.
 int i8_launch(const i8_problem* d_probs, const I8Epi* d_epi, const void* d_sched, const i8_sched_info* info,
               hipStream_t s, int kernel = kI8General);
@@ -206,4 +216,6 @@ struct ggemm_handle_s {
   int i8_mode;         // GGEMM_I8_KERNEL at create: 0 automatic, 1 general kernel only, 2 large-tile kernel
                        // only, the kernel-level layouts (testing)
   int f64_tile;        // GGEMM_F64_TILE at create: 0 automatic, 64 or 128 forces the native GEMM's tile edge
+  int packed_max_kp;   // GGEMM_PACKED_MAX_KP at create: calls whose largest Kp is at most this use packed residues
+  int i8_persistent;   // GGEMM_I8_SCHED=persistent at create: the persistent work-stealing INT8 kernels
 };

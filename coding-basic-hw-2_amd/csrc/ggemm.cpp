@@ -233,7 +233,7 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
   // with the blocked digits); at k = 16384 the row-major planes stream better (5 % slower packed).
   int max_kp = 0;
   for (int j = 0; j < c.ne; ++j) max_kp = std::max(max_kp, kp_of(probs[emu_idx[j]].k));
-  c.packed = !h->digits_colmajor && max_kp <= kPackedMaxKp;
+  c.packed = !h->digits_colmajor && max_kp <= h->packed_max_kp;
   if (c.blocked) SY = SYb;
   uint8_t* ybase = reinterpret_cast<uint8_t*>(h->C32);
   int32_t* lbase = reinterpret_cast<int32_t*>(ybase + (size_t)nmax * SY);
@@ -320,7 +320,7 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
   if (c.nn && f64_build_schedule(hf, c.nn, hb + c.L.off_sf64, s_f64, &c.f64_tiles, nullptr, h->f64_tile))
     return GGEMM_ERR_INVALID;
   if (c.ne && i8_build_schedule(hi8, (int)c.n_i8, hb + c.L.off_si8, s_i8, &c.i8info, h->num_cus, large_mode(h, c),
-                                   &c.i8_kernel))
+                                   &c.i8_kernel, h->i8_persistent != 0))
     return GGEMM_ERR_I8GEMM;
   c.h2d_bytes = c.ne ? c.L.off_si8 + c.i8info.bytes_used : c.L.off_si8;
   *out = c;
@@ -483,10 +483,13 @@ int path_emu_loop(ggemm_handle_t h, bool batched, const ggemm_problem_t* probs, 
   for (int j = 0; j < c.ne && !r; ++j) {
     const int planes = hoz[j].num_moduli + OZ2_EXTRA_PLANES;
     if (batched) {
-      if (i8_build_schedule(hi8 + q, planes, hb + base + j * per, per, &h->loop_info[j], h->num_cus)) r = GGEMM_ERR_I8GEMM;
+      if (i8_build_schedule(hi8 + q, planes, hb + base + j * per, per, &h->loop_info[j], h->num_cus, kLargeNever,
+                            nullptr, h->i8_persistent != 0))
+        r = GGEMM_ERR_I8GEMM;
     } else {
       for (int l = 0; l < planes && !r; ++l)
-        if (i8_build_schedule(hi8 + q + l, 1, hb + base + (q + l) * per, per, &h->loop_info[q + l], h->num_cus))
+        if (i8_build_schedule(hi8 + q + l, 1, hb + base + (q + l) * per, per, &h->loop_info[q + l], h->num_cus,
+                              kLargeNever, nullptr, h->i8_persistent != 0))
           r = GGEMM_ERR_I8GEMM;
     }
     q += planes;
@@ -498,6 +501,7 @@ int path_emu_loop(ggemm_handle_t h, bool batched, const ggemm_problem_t* probs, 
   const i8_problem* di8 = reinterpret_cast<const i8_problem*>(db + c.L.off_i8);
   const I8Epi* depi = reinterpret_cast<const I8Epi*>(db + c.L.off_epi);
   q = 0;
+  const int i8k = h->i8_persistent ? kI8Persistent : kI8General;
   for (int j = 0; j < c.ne && !r; ++j) {
     const int planes = hoz[j].num_moduli + OZ2_EXTRA_PLANES;
     if (prep_launch(doz + j, 1, hoz[j].m, hoz[j].n, h->stream, 1, c.packed, hoz[j].num_moduli)) {
@@ -506,11 +510,14 @@ int path_emu_loop(ggemm_handle_t h, bool batched, const ggemm_problem_t* probs, 
     }
     ++nl;
     if (batched) {
-      if (i8_launch(di8 + q, depi + q, db + base + j * per, &h->loop_info[j], h->stream)) { r = GGEMM_ERR_I8GEMM; break; }
+      if (i8_launch(di8 + q, depi + q, db + base + j * per, &h->loop_info[j], h->stream, i8k)) {
+        r = GGEMM_ERR_I8GEMM;
+        break;
+      }
       nl += h->loop_info[j].num_launches;
     } else {
       for (int l = 0; l < planes && !r; ++l) {
-        if (i8_launch(di8 + q + l, depi + q + l, db + base + (q + l) * per, &h->loop_info[q + l], h->stream))
+        if (i8_launch(di8 + q + l, depi + q + l, db + base + (q + l) * per, &h->loop_info[q + l], h->stream, i8k))
           r = GGEMM_ERR_I8GEMM;
         else nl += h->loop_info[q + l].num_launches;
       }
@@ -599,6 +606,8 @@ extern "C" const char* ggemm_profile_i8_kernel(void) {
   switch (ggemm::prof::last_i8) {
     case ggemm::kI8General: return "i8_grouped_kernel";
     case ggemm::kI8Large: return "i8_large_kernel";
+    case ggemm::kI8General | ggemm::kI8Persistent: return "i8_grouped_persistent_kernel";
+    case ggemm::kI8Large | ggemm::kI8Persistent: return "i8_large_persistent_kernel";
     default: return "";
   }
 }
@@ -702,6 +711,10 @@ extern "C" int ggemm_create_ex(ggemm_handle_t* out, int max_problems, size_t max
   h->f64_tile = !et ? 0 : std::atoi(et) == 64 ? 64 : std::atoi(et) == 128 ? 128 : 0;
   const char* e = std::getenv("GGEMM_STATS_REPAIR");
   h->stats_repair = (e && std::atoi(e) == 1) ? 1 : 0;
+  const char* esc = std::getenv("GGEMM_I8_SCHED");
+  h->i8_persistent = (esc && !std::strcmp(esc, "persistent")) ? 1 : 0;
+  const char* epk = std::getenv("GGEMM_PACKED_MAX_KP");
+  h->packed_max_kp = epk ? std::max(0, std::atoi(epk)) : kPackedMaxKp;
   if (hipStreamSynchronize(stream) != hipSuccess) FAIL(GGEMM_ERR_CUDA);
 #undef HIPA
 #undef FAIL

@@ -3,18 +3,20 @@
 // Problem (src/int8_grouped_gemm.h:4-10 layout): A m x kp and B n x kp row-major (K contiguous),
 // C = A B^T column-major m x n (ld m), kp % 32 == 0, |C| <= 128^2 kp < 2^31 (kp <= 131040).
 //
-// One launch covers every (problem, plane) of a group.  The host builds a tile table in
-// longest-processing-time order (heaviest tiles first, the reference's scheduling contract,
-// src/int8_grouped_gemm.cu:602-675).  Workgroup b takes one tile:
-//   * XCD-aware dispatch: MI355X deals workgroups round-robin to its 8 XCDs (b mod 8), each with
-//     its own L2.  Workgroup b is mapped to tile chunk (b mod 8) + 8 (b / (8 C)) of C
-//     consecutive table tiles, so one XCD works through contiguous runs of the table;
-//   * inside an entry tiles are rastered in groups of G tile-rows, m fastest, so the compute
-//     units of an XCD share A and B panels in L2.
-//   General kernel C = 32, G = 8: a 1024^2 product's 32 tiles share one L2 and each plane is read
-//   from HBM once (C = 16 reads them 1.5 times at equal speed).  Large-tile kernel C = 16, G = 4:
-//   on 8192^2 x 16384 products 1-3 % faster than 32 / 8 in two of three same-box comparisons,
-//   equal in the third (G = 16: 10 % slower).
+// One launch covers every (problem, plane) of a group, with persistent workgroups and a
+// work-stealing tile scheduler (the reference's contract, src/int8_grouped_gemm.cu:360-407 and
+// :602-675).  The host builds a tile table in longest-processing-time order (heaviest tiles
+// first) and deals its entries -- whole (problem, plane) products -- to eight queues, one per XCD
+// (MI355X deals workgroups round-robin to its 8 XCDs, b mod 8, each with its own L2): a product's
+// residue panels are then read from HBM by one XCD only and shared through its L2 (on 8192^2 x
+// 16384 products, spreading each product over all XCDs read 6.3 times the planes' bytes from HBM).
+// A workgroup takes tiles from its own XCD's queue by an atomic counter, fetched one tile ahead,
+// and once that queue is exhausted steals from the others in turn; the last workgroup to finish
+// resets the counters.  Inside a product tiles are rastered in groups of G tile-rows, m fastest,
+// so the compute units of an XCD share A and B panels in L2 (general kernel G = 8, large-tile
+// kernel G = 4).  When a tile's last k-stage is in registers, the workgroup issues the next tile's
+// first stages into the free LDS ring before its epilogue, so the operand stream does not drain
+// between tiles.
 // General kernel: workgroups of 512 threads = 8 waves in a 4 x 2 arrangement, two workgroups per
 // compute unit (one's epilogue and barrier waits overlap the other's MFMA work):
 //   cfg 0: 256 x 128 tile, wave tile 64 x 64 = 4 x 4 blocks of v_mfma_i32_16x16x64_i8
@@ -41,6 +43,7 @@
 // contiguous 256-byte (digits) or 1 KB (int32) store instead of 16 column pieces.
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <type_traits>
@@ -58,14 +61,14 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kBK = 64;
-// XCD chunk (tiles) and raster group (tile-rows) of the two kernels
-constexpr int kChunk = 32, kGroupM = 8;     // general kernel
-constexpr int kChunkL = 16, kGroupML = 4;   // large-tile kernel
-constexpr int kXcds = 8;
+// raster group (tile-rows) of the two kernels
+constexpr int kGroupM = 8;    // general kernel
+constexpr int kGroupML = 4;   // large-tile kernel
 
 // Tile BM x BN computed by WGM x WGN waves through an NST-stage LDS ring.
-template <int BM_, int BN_, int WGM_, int WGN_, int NST_>
+template <int ID_, int BM_, int BN_, int WGM_, int WGN_, int NST_>
 struct Cfg {
+  static constexpr int ID = ID_;   // tile configuration number in the schedule's entries
   static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_, NST = NST_;
   static constexpr int NW = WGM * WGN, NT = 64 * NW;
   static constexpr int WM = BM / WGM, WN = BN / WGN;   // wave tile
@@ -84,15 +87,15 @@ struct Cfg {
 // general kernel: 512 threads = 8 waves of (BM / 4) x (BN / 2), two workgroups per compute unit
 // (72 KB of LDS each, four waves per SIMD); against 4 waves of (BM / 2) x (BN / 2) the 256 x 128
 // tiles of 1024^3 products run 1.4-3 % faster (more waves hide the DMA and LDS waits)
-using Cfg0 = Cfg<256, 128, 4, 2, 3>;
-using Cfg1 = Cfg<128, 128, 4, 2, 3>;
-using Cfg2 = Cfg<64, 64, 4, 2, 3>;
+using Cfg0 = Cfg<0, 256, 128, 4, 2, 3>;
+using Cfg1 = Cfg<1, 128, 128, 4, 2, 3>;
+using Cfg2 = Cfg<2, 64, 64, 4, 2, 3>;
 constexpr int kThreads = 512;
 constexpr int kSmem = Cfg0::SMEM;
 static_assert(Cfg1::SMEM <= kSmem && Cfg2::SMEM <= kSmem, "smem");
 // large-tile kernel: 1024 threads = 16 waves of 64 x 64 (4 per SIMD, so one wave's LDS reads and
 // barrier waits overlap the others' MFMAs), one workgroup per compute unit, 128 KB ring
-using CfgL = Cfg<256, 256, 4, 4, 4>;
+using CfgL = Cfg<0, 256, 256, 4, 4, 4>;
 constexpr int kThreadsL = CfgL::NT;
 constexpr int kSmemL = CfgL::SMEM;
 
@@ -308,30 +311,98 @@ __device__ __forceinline__ void tile_epilogue(const v4i (&acc)[C::FM][C::FN], co
   });
 }
 
+// threadIdx.x, opaque to the optimizer: per-lane values derived from it are computed per tile
+// instead of being hoisted out of the persistent loop (one set per tile configuration, live
+// throughout, took the kernels past their register budget)
+__device__ __forceinline__ int tile_tid() {
+  int t = threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+
+// Operand stream of one tile: the DMA of its k-stage kt into an LDS ring slot.
 template <class C, bool kPacked>
-__device__ __forceinline__ void run_tile(uint8_t* lds, const i8_problem& P, const I8Epi& epi, int tm, int tn) {
-  constexpr int FM = C::FM, FN = C::FN, NST = C::NST;
-  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave % C::WGM, wn = wave / C::WGM;
-  const int row0 = tm * C::BM, col0 = tn * C::BN;
-  const int m_rem = P.m - row0, n_rem = P.n - col0;
-  const int kp = P.kp;
-  const int nk = (kp + kBK - 1) / kBK;
-  // full stages: all tile rows exist and the stage has 64 bytes per row (packed: every k-block but
-  // a final half block; row-major: every stage but a final half stage)
-  const bool full_rows = m_rem >= C::BM && n_rem >= C::BN;
-  const int fstride = kPacked ? 64 : kp;
-  const int r_in = lane >> 2;
-  const uint32_t lane_off = (uint32_t)(r_in * fstride + 16 * swz(r_in, lane & 3));
-  auto load = [&](int kt, uint8_t* st) {
+struct TileSrc {
+  const int8_t* A;
+  const int8_t* B;
+  int m, n, kp, row0, col0, m_rem, n_rem;
+  bool full_rows;
+  uint32_t lane_off;
+  int wave, lane;
+  __device__ __forceinline__ TileSrc(const i8_problem& P, int tm, int tn)
+      : A(P.A), B(P.B), m(P.m), n(P.n), kp(P.kp), row0(tm * C::BM), col0(tn * C::BN), m_rem(P.m - tm * C::BM),
+        n_rem(P.n - tn * C::BN) {
+    const int tid = tile_tid();
+    lane = tid & 63;
+    wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // full stages: all tile rows exist and the stage has 64 bytes per row (packed: every k-block but
+    // a final half block; row-major: every stage but a final half stage)
+    full_rows = m_rem >= C::BM && n_rem >= C::BN;
+    const int fstride = kPacked ? 64 : kp;
+    const int r_in = lane >> 2;
+    lane_off = (uint32_t)(r_in * fstride + 16 * swz(r_in, lane & 3));
+  }
+  __device__ __forceinline__ void load(int kt, uint8_t* st) const {
     const int k0 = kt * kBK;
     if (full_rows && k0 + kBK <= kp) {
-      const int8_t* a = kPacked ? P.A + (size_t)(k0 >> 6) * P.m * 64 + (size_t)row0 * 64 : P.A + (size_t)row0 * kp + k0;
-      const int8_t* b = kPacked ? P.B + (size_t)(k0 >> 6) * P.n * 64 + (size_t)col0 * 64 : P.B + (size_t)col0 * kp + k0;
-      dma_stage_full<C>(a, b, fstride, fstride, lane_off, lane_off, st, wave);
+      const int8_t* a = kPacked ? A + (size_t)(k0 >> 6) * m * 64 + (size_t)row0 * 64 : A + (size_t)row0 * kp + k0;
+      const int8_t* b = kPacked ? B + (size_t)(k0 >> 6) * n * 64 + (size_t)col0 * 64 : B + (size_t)col0 * kp + k0;
+      dma_stage_full<C>(a, b, kPacked ? 64 : kp, kPacked ? 64 : kp, lane_off, lane_off, st, wave);
     } else {
-      dma_stage<C>(stage_src(P.A, P.m, row0, kp, k0, kPacked), stage_src(P.B, P.n, col0, kp, k0, kPacked), m_rem,
-                   n_rem, st, wave, lane);
+      dma_stage<C>(stage_src(A, m, row0, kp, k0, kPacked), stage_src(B, n, col0, kp, k0, kPacked), m_rem, n_rem, st,
+                   wave, lane);
+    }
+  }
+  // the stages a tile's k loop expects in flight when it starts (ring slots 0, 1, ...): NST with the
+  // split loop, NST - 1 otherwise
+  __device__ __forceinline__ void prologue(uint8_t* lds) const {
+    constexpr int PRE = C::kSplit ? C::NST : C::NST - 1;
+    const int nk = (kp + kBK - 1) / kBK;
+#pragma unroll
+    for (int q = 0; q < PRE; ++q)
+      if (q < nk) load(q, lds + q * C::STAGE);
+  }
+};
+
+__device__ __forceinline__ I8Epi epi_of(const I8Epi* __restrict__ epis, int pi) {
+  return epis ? epis[pi] : I8Epi{0u, 1u, 0u, 0u};
+}
+
+// A unit of the persistent schedule, decoded: one tile (tm, tn) of product pi (< 0: none).
+struct Unit {
+  int pi, cfg, tm, tn;
+};
+
+// One tile: the k loop over its stages and the epilogue.  The tile's prologue stages (TileSrc::
+// prologue) are in flight when it starts.  kFresh: they are this workgroup's only memory operations
+// in flight (a workgroup that runs one tile), so the first wait lets the later prologue stages
+// stay in flight; otherwise (persistent workgroups) the previous tile's epilogue stores may be
+// in flight too, and the first wait is a full one.
+// claim(): called by every thread once, after the tile's last stage has landed (no operand load of
+// this tile is in flight any more); it starts the fetch of the workgroup's next unit.  next():
+// called by every thread once, after the last stage's MFMAs are issued and before the epilogue; it
+// passes a workgroup barrier, after which no wave reads this tile's LDS ring, and returns the next
+// unit.  When that unit has this tile's configuration its prologue is issued here, ahead of the
+// epilogue (returns true), so the operand ring keeps streaming across tiles.
+template <class C, bool kPacked, bool kFresh, class Claim, class Next>
+__device__ __forceinline__ bool run_tile(uint8_t* lds, const i8_problem* __restrict__ probs,
+                                         const I8Epi* __restrict__ epis, int pi, int tm, int tn, Claim&& claim,
+                                         Next&& next) {
+  const i8_problem& P = probs[pi];
+  const I8Epi epi = epi_of(epis, pi);
+  constexpr int FM = C::FM, FN = C::FN, NST = C::NST;
+  const TileSrc<C, kPacked> src(P, tm, tn);
+  const int tid = tile_tid(), lane = tid & 63, wave = src.wave;
+  const int wm = wave % C::WGM, wn = wave / C::WGM;
+  const int kp = P.kp;
+  const int nk = (kp + kBK - 1) / kBK;
+  __builtin_assume(nk > 0);   // scheduled tiles have kp > 0
+  bool prefetched = false;
+  auto handoff = [&]() {
+    const Unit nx = next();
+    if (nx.pi >= 0 && nx.cfg == C::ID && ((epi_of(epis, nx.pi).mode & kEpiPacked) != 0) == kPacked) {
+      TileSrc<C, kPacked>(probs[nx.pi], nx.tm, nx.tn).prologue(lds);
+      prefetched = true;
     }
   };
 
@@ -371,13 +442,9 @@ __device__ __forceinline__ void run_tile(uint8_t* lds, const i8_problem& P, cons
     // registers just consumed, issues the second half and reads the rest of stage kt + 1.  The
     // barrier and the LDS latency overlap queued MFMA work (16-wave kernel: 2.4 % at k = 16384).
     constexpr int H = FM / 2;
-#pragma unroll
-    for (int q = 0; q < NST; ++q)
-      if (q < nk) load(q, lds + q * C::STAGE);
-    if (nk <= 0) return;      // never scheduled: problems with kp == 0 get no tiles
-    __builtin_assume(nk > 0);  // one path into the epilogue (no zero-trip copy of the accumulators)
-    // stage 0 landed (stages 1 .. NST - 1 may still be in flight)
-    if (NST - 1 < nk) wait_barrier<(NST - 1) * C::VM>(); else wait_barrier<0>();
+    // stage 0 landed (with kFresh, stages 1 .. NST - 1 may still be in flight)
+    if (kFresh && NST - 1 < nk) wait_barrier<(NST - 1) * C::VM>(); else wait_barrier<0>();
+    if (nk == 1) claim();
     if (nk == 1 && (kp & 63)) {
       zero_half(lds);
       wait_barrier<0>();
@@ -396,7 +463,8 @@ __device__ __forceinline__ void run_tile(uint8_t* lds, const i8_problem& P, cons
         // stage kt + 1 landed (the NST - 2 stages after it may still be in flight; near the end
         // fewer were issued, so wait for everything)
         if (kt + NST - 1 < nk) wait_barrier<(NST - 2) * C::VM>(); else wait_barrier<0>();
-        if (kt + NST < nk) load(kt + NST, lds + buf * C::STAGE);
+        if (kt + 2 == nk) claim();   // the last stage landed
+        if (kt + NST < nk) src.load(kt + NST, lds + buf * C::STAGE);
         if (kt + 2 == nk && (kp & 63)) {
           zero_half(lds + nb * C::STAGE);
           wait_barrier<0>();
@@ -413,24 +481,21 @@ __device__ __forceinline__ void run_tile(uint8_t* lds, const i8_problem& P, cons
     // the last iteration issues no reads: an explicit wait keeps every path into the epilogue
     // free of pending LDS loads (also for the assembly dataflow check)
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    handoff();   // every wave has issued the last stage's MFMAs: the ring is free
   } else {
     // Stage kt waits, passes the barrier (every wave is done with stage kt - 1), refills slot
     // kt - 1 with stage kt + NST - 1, reads all its fragments and issues every MFMA.  With two
     // workgroups per compute unit the other workgroup's MFMAs cover this one's waits.
-#pragma unroll
-    for (int q = 0; q < NST - 1; ++q)
-      if (q < nk) load(q, lds + q * C::STAGE);
     int buf = 0;
-    if (nk <= 0) return;      // never scheduled: problems with kp == 0 get no tiles
-    __builtin_assume(nk > 0);  // one path into the epilogue (no zero-trip copy of the accumulators)
     for (int kt = 0; kt < nk; ++kt) {
       // stage kt landed (the NST - 2 stages after it may still be in flight; near the end fewer
-      // were issued, so wait for everything) and every wave is done with stage kt - 1
-      if (kt + NST - 2 < nk) wait_barrier<(NST - 2) * C::VM>(); else wait_barrier<0>();
+      // were issued, and at kt = 0 the previous tile's stores may be, so wait for everything) and
+      // every wave is done with stage kt - 1
+      if ((kFresh || kt > 0) && kt + NST - 2 < nk) wait_barrier<(NST - 2) * C::VM>(); else wait_barrier<0>();
       if (kt + NST - 1 < nk) {
         int b2 = buf + NST - 1;   // the ring slot of stage kt - 1
         if (b2 >= NST) b2 -= NST;
-        load(kt + NST - 1, lds + b2 * C::STAGE);
+        src.load(kt + NST - 1, lds + b2 * C::STAGE);
       }
       if (kt == nk - 1 && (kp & 63)) {
         zero_half(lds + buf * C::STAGE);
@@ -449,45 +514,35 @@ __device__ __forceinline__ void run_tile(uint8_t* lds, const i8_problem& P, cons
       __builtin_amdgcn_s_setprio(0);
       buf = buf + 1 == NST ? 0 : buf + 1;
     }
+    // after the last MFMAs (a claim any earlier in this loop took the kernel past 128 VGPRs, i.e.
+    // one workgroup per compute unit); the other workgroup's MFMAs cover the fetch
+    claim();
+    handoff();   // every wave has issued the last stage's MFMAs: the ring is free
   }
 
-  tile_epilogue<C>(acc, P, epi, row0, col0, wave, lane);
+  // the epilogue's descriptor fields are read again here rather than kept live through the k loop
+  int pi_e = pi;
+  asm volatile("" : "+s"(pi_e));
+  tile_epilogue<C>(acc, probs[pi_e], epi_of(epis, pi_e), src.row0, src.col0, wave, lane);
+  return prefetched;
 }
 
-// Tile of workgroup blockIdx.x: XCD-aware remap of the dispatch index (a permutation of
-// [0, total)) and entry lookup in the prefix table; `local` is the tile index inside the entry.
-struct TileRef {
-  int pi, cfg, local;
-};
-template <int CH>
-__device__ __forceinline__ TileRef find_tile(const int* __restrict__ sched) {
-  const int total = sched[0];
-  const int ne = sched[1];
-  const int b = blockIdx.x;
-  const int span = kXcds * CH;
-  const int full = total / span * span;
-  int tile = b;
-  if (b < full) {
-    const int x = b % kXcds, q = b / kXcds;
-    tile = (q / CH) * span + x * CH + (q % CH);
-  }
-  const int* prefix = sched + kSchedHdr;
-  const int* entry = prefix + ne + 1;
-  const int per = sched[2];   // tiles of every entry when they are all equal (no search), else 0
-  int lo;
-  if (per > 0) {
-    lo = tile / per;
-  } else {
-    lo = 0;                   // largest e with prefix[e] <= tile
-    int hi = ne - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (prefix[mid] <= tile) lo = mid; else hi = mid - 1;
-    }
-  }
-  const int e = entry[lo];
-  return TileRef{e >> 2, e & 3, tile - (per > 0 ? lo * per : prefix[lo])};
-}
+// ---------------------------------------------------------------- persistent tile scheduler
+// Schedule image (ints; built by i8_build_schedule):
+//   [0] units (tiles) in all, [1] entries, [2] tiles per entry when all entries have the same count
+//   (else 0), [3] chunk c (> 0: queue x is chunks x, x + 8, ... of c consecutive units instead of a
+//   range); [kHdrXcd + x], x = 0..8: first unit of XCD x's queue (x = 8: the total);
+//   [kHdrCtr + x], x < 8: XCD x's queue counter, [kHdrDone]: workgroups finished -- zero in the
+//   uploaded image and reset by the last workgroup of every launch, so a captured graph replays
+//   without clearing them; prefix[entries + 1] at kSchedHdr (first unit of each entry),
+//   entry[entries] = (problem << 2) | tile config.
+// Entries (whole (problem, plane) products) are dealt to the eight XCD queues by the host, heaviest
+// first onto the least loaded queue, so a product's residue panels are read from HBM by one XCD
+// and shared in its L2; a workgroup takes the units of its own XCD's queue (blockIdx mod 8: the
+// dispatcher deals workgroups to the XCDs round-robin) through the queue counter and, once that
+// is exhausted, steals from the other queues in turn.
+static_assert(kHdrDone < kSchedHdr, "schedule header");
+
 // grouped raster inside a product: blocks of GM tile-rows, m fastest inside a block
 template <int GM>
 __device__ __forceinline__ void raster(int local, int m, int n, int bm, int bn, int& tm, int& tn) {
@@ -499,37 +554,199 @@ __device__ __forceinline__ void raster(int local, int m, int n, int bm, int bn, 
   tm = first_m + r % gsz;
   tn = r / gsz;
 }
+// unit u (wave-uniform, >= 0) -> problem, tile configuration and tile position
+template <int GM, bool kLarge>
+__device__ __forceinline__ Unit decode_unit(const int* __restrict__ sched, const i8_problem* __restrict__ probs, int u) {
+  const int ne = sched[1], per = sched[2];
+  const int* prefix = sched + kSchedHdr;
+  const int* entry = prefix + ne + 1;
+  int e, local;
+  if (per > 0) {
+    e = u / per;
+    local = u - e * per;
+  } else {
+    int lo = 0, hi = ne - 1;   // largest e with prefix[e] <= u
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (prefix[mid] <= u) lo = mid; else hi = mid - 1;
+    }
+    e = lo;
+    local = u - prefix[lo];
+  }
+  const int ev = entry[e];
+  Unit t;
+  t.pi = ev >> 2;
+  t.cfg = ev & 3;
+  raster<GM>(local, probs[t.pi].m, probs[t.pi].n, kLarge ? 256 : i8_tile_m(t.cfg), kLarge ? 256 : i8_tile_n(t.cfg),
+             t.tm, t.tn);
+  return t;
+}
+// the next local index of queue q from its counter: past the n_q workgroups' first tiles
+__device__ __forceinline__ int fetch_local(int* __restrict__ sched, int q) {
+  const int nq = ((int)gridDim.x - q + kXcds - 1) / kXcds;
+  return atomicAdd(sched + kHdrCtr + q, 1) + nq;
+}
+// Thread 0 only.  Queue q's units in order are its local indices 0, 1, ...; the workgroups of XCD q
+// (blockIdx = q mod 8, n_q of them) start on local indices 0 .. n_q - 1 without a fetch, and a
+// value v fetched from the queue's counter names local index n_q + v.  So the first round of tiles
+// of an XCD is one contiguous run of its queue, as every later round is approximately (a fetch that
+// raced ahead of other workgroups' first tiles would scatter the first round over twice as many
+// products, more than the XCD's L2 holds).  l: a local index of the queue qi steps after the own
+// one.  Returns the unit it names or, when that queue is exhausted, moves to the next queue (the
+// own XCD's first, then the others in turn, each once) and fetches again; -1 when all are
+// exhausted.
+__device__ __forceinline__ int resolve_unit(int* __restrict__ sched, int own, int& qi, int l) {
+  const int ch = sched[3];
+  for (;;) {
+    const int q = (own + qi) & (kXcds - 1);
+    if (ch > 0) {   // queue q: chunks q, q + 8, q + 16, ... of ch consecutive units
+      const int u = ((l / ch) * kXcds + q) * ch + l % ch;
+      if (u < sched[0]) return u;
+    } else {        // queue q: the units [first(q), first(q + 1))
+      const int u = sched[kHdrXcd + q] + l;
+      if (u < sched[kHdrXcd + q + 1]) return u;
+    }
+    if (++qi == kXcds) return -1;
+    l = fetch_local(sched, (own + qi) & (kXcds - 1));
+  }
+}
+
+// The persistent workgroup: takes units until every queue is exhausted.  The next unit is fetched
+// when the current tile's last stage has landed (its counter atomic then overlaps the last stage's
+// MFMAs; fetched any earlier, the claims of an XCD's workgroups interleave across rounds and its
+// tiles in flight span more products than its L2 holds -- measured 1.6 times the HBM reads), and
+// handed to the current tile before its epilogue.  pro(unit) issues a unit's prologue; run(unit,
+// claim, next) runs one unit and returns whether it issued the next unit's prologue.
+template <int GM, bool kLarge, class Pro, class Run>
+__device__ __forceinline__ void persistent(int* __restrict__ sched, const i8_problem* __restrict__ probs, Pro&& pro,
+                                           Run&& run) {
+  __shared__ int s_unit[2];
+  const int tid = threadIdx.x;
+  const int own = blockIdx.x & (kXcds - 1);
+  int qi = 0, pend = 0;   // thread 0: queues exhausted so far, the local index of the fetch in flight
+  if (tid == 0) s_unit[0] = resolve_unit(sched, own, qi, (int)blockIdx.x / kXcds);
+  __syncthreads();
+  const int u0 = __builtin_amdgcn_readfirstlane(s_unit[0]);
+  Unit cur{-1, 0, 0, 0};
+  if (u0 >= 0) cur = decode_unit<GM, kLarge>(sched, probs, u0);
+  bool pre = false;
+  for (int it = 1; cur.pi >= 0; ++it) {
+    Unit nxt{-1, 0, 0, 0};
+    auto claim = [&]() {
+      if (tid == 0 && qi < kXcds) pend = fetch_local(sched, (own + qi) & (kXcds - 1));
+    };
+    auto next = [&]() -> Unit {
+      if (tid == 0) s_unit[it & 1] = qi < kXcds ? resolve_unit(sched, own, qi, pend) : -1;
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      const int nu = __builtin_amdgcn_readfirstlane(s_unit[it & 1]);
+      if (nu >= 0) nxt = decode_unit<GM, kLarge>(sched, probs, nu);
+      return nxt;
+    };
+    if (!pre) pro(cur);
+    pre = run(cur, claim, next);
+    cur = nxt;
+  }
+  // every fetch of this workgroup has returned (its value was used): the last workgroup to finish
+  // resets the queue counters for the next launch
+  if (tid == 0) {
+    __threadfence();
+    if (atomicAdd(sched + kHdrDone, 1) == (int)gridDim.x - 1) {
+      for (int x = 0; x < kXcds; ++x) atomicExch(sched + kHdrCtr + x, 0);
+      atomicExch(sched + kHdrDone, 0);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- hardware-dispatched kernels
+// One workgroup per tile; the dispatcher hands workgroups to free compute-unit slots in index order,
+// i.e. the tiles in LPT order to whichever unit frees first -- the same greedy list schedule as the
+// persistent kernel's queue, kept by the command processor (measured faster on MI355X, see the
+// launcher).  Workgroup b takes tile chunk (b mod 8) + 8 (b / (8 CH)) of CH consecutive tiles of the
+// table, so one XCD works through contiguous runs (general kernel CH = 32: a 1024^2 product's 32
+// tiles share one L2 and each plane is read from HBM once; large-tile kernel CH = 16).
+constexpr int kChunk = 32, kChunkL = 16;
+template <int CH>
+__device__ __forceinline__ int dispatched_unit(const int* __restrict__ sched) {
+  const int total = sched[0];
+  const int b = blockIdx.x;
+  const int span = kXcds * CH;
+  const int full = total / span * span;
+  if (b >= full) return b;
+  const int x = b % kXcds, q = b / kXcds;
+  return (q / CH) * span + x * CH + (q % CH);
+}
+template <class C, bool kPacked>
+__device__ __forceinline__ void one_tile(uint8_t* lds, const i8_problem* __restrict__ probs,
+                                         const I8Epi* __restrict__ epis, const Unit& t) {
+  TileSrc<C, kPacked>(probs[t.pi], t.tm, t.tn).prologue(lds);
+  run_tile<C, kPacked, true>(lds, probs, epis, t.pi, t.tm, t.tn, [] {}, [] { return Unit{-1, 0, 0, 0}; });
+}
 
 __global__ void __launch_bounds__(kThreads, 2) i8_grouped_kernel(const i8_problem* __restrict__ probs,
                                                                  const I8Epi* __restrict__ epis,
-                                                                 const int* __restrict__ sched) {
+                                                                 int* __restrict__ sched) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
-  const TileRef t = find_tile<kChunk>(sched);
-  const i8_problem P = probs[t.pi];
-  I8Epi epi{0u, 1u, 0u, 0u};
-  if (epis) epi = epis[t.pi];
-  int tm, tn;
-  raster<kGroupM>(t.local, P.m, P.n, i8_tile_m(t.cfg), i8_tile_n(t.cfg), tm, tn);
+  const Unit t = decode_unit<kGroupM, false>(sched, probs, dispatched_unit<kChunk>(sched));
+  const bool pk = (epi_of(epis, t.pi).mode & kEpiPacked) != 0;
   switch (t.cfg) {
-    case 0: (epi.mode & kEpiPacked) ? run_tile<Cfg0, true>(lds, P, epi, tm, tn) : run_tile<Cfg0, false>(lds, P, epi, tm, tn); break;
-    case 1: (epi.mode & kEpiPacked) ? run_tile<Cfg1, true>(lds, P, epi, tm, tn) : run_tile<Cfg1, false>(lds, P, epi, tm, tn); break;
-    default: (epi.mode & kEpiPacked) ? run_tile<Cfg2, true>(lds, P, epi, tm, tn) : run_tile<Cfg2, false>(lds, P, epi, tm, tn); break;
+    case 0: pk ? one_tile<Cfg0, true>(lds, probs, epis, t) : one_tile<Cfg0, false>(lds, probs, epis, t); break;
+    case 1: pk ? one_tile<Cfg1, true>(lds, probs, epis, t) : one_tile<Cfg1, false>(lds, probs, epis, t); break;
+    default: pk ? one_tile<Cfg2, true>(lds, probs, epis, t) : one_tile<Cfg2, false>(lds, probs, epis, t); break;
   }
 }
 
 // every tile of the schedule is a 256 x 256 tile
 __global__ void __launch_bounds__(kThreadsL, 1) i8_large_kernel(const i8_problem* __restrict__ probs,
                                                                 const I8Epi* __restrict__ epis,
-                                                                const int* __restrict__ sched) {
+                                                                int* __restrict__ sched) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
-  const TileRef t = find_tile<kChunkL>(sched);
-  const i8_problem P = probs[t.pi];
-  I8Epi epi{0u, 1u, 0u, 0u};
-  if (epis) epi = epis[t.pi];
-  int tm, tn;
-  raster<kGroupML>(t.local, P.m, P.n, CfgL::BM, CfgL::BN, tm, tn);
-  if (epi.mode & kEpiPacked) run_tile<CfgL, true>(lds, P, epi, tm, tn);
-  else run_tile<CfgL, false>(lds, P, epi, tm, tn);
+  const Unit t = decode_unit<kGroupML, true>(sched, probs, dispatched_unit<kChunkL>(sched));
+  if (epi_of(epis, t.pi).mode & kEpiPacked) one_tile<CfgL, true>(lds, probs, epis, t);
+  else one_tile<CfgL, false>(lds, probs, epis, t);
+}
+
+// ---------------------------------------------------------------- persistent kernels
+__global__ void __launch_bounds__(kThreads, 2) i8_grouped_persistent_kernel(const i8_problem* __restrict__ probs,
+                                                                            const I8Epi* __restrict__ epis,
+                                                                            int* __restrict__ sched) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+  auto pro = [&](const Unit& t) {
+    const bool pk = (epi_of(epis, t.pi).mode & kEpiPacked) != 0;
+    switch (t.cfg) {
+      case 0: pk ? TileSrc<Cfg0, true>(probs[t.pi], t.tm, t.tn).prologue(lds)
+                 : TileSrc<Cfg0, false>(probs[t.pi], t.tm, t.tn).prologue(lds); break;
+      case 1: pk ? TileSrc<Cfg1, true>(probs[t.pi], t.tm, t.tn).prologue(lds)
+                 : TileSrc<Cfg1, false>(probs[t.pi], t.tm, t.tn).prologue(lds); break;
+      default: pk ? TileSrc<Cfg2, true>(probs[t.pi], t.tm, t.tn).prologue(lds)
+                  : TileSrc<Cfg2, false>(probs[t.pi], t.tm, t.tn).prologue(lds); break;
+    }
+  };
+  persistent<kGroupM, false>(sched, probs, pro, [&](const Unit& t, auto& claim, auto& next) -> bool {
+    const bool pk = (epi_of(epis, t.pi).mode & kEpiPacked) != 0;
+    switch (t.cfg) {
+      case 0: return pk ? run_tile<Cfg0, true, false>(lds, probs, epis, t.pi, t.tm, t.tn, claim, next)
+                        : run_tile<Cfg0, false, false>(lds, probs, epis, t.pi, t.tm, t.tn, claim, next);
+      case 1: return pk ? run_tile<Cfg1, true, false>(lds, probs, epis, t.pi, t.tm, t.tn, claim, next)
+                        : run_tile<Cfg1, false, false>(lds, probs, epis, t.pi, t.tm, t.tn, claim, next);
+      default: return pk ? run_tile<Cfg2, true, false>(lds, probs, epis, t.pi, t.tm, t.tn, claim, next)
+                         : run_tile<Cfg2, false, false>(lds, probs, epis, t.pi, t.tm, t.tn, claim, next);
+    }
+  });
+}
+
+__global__ void __launch_bounds__(kThreadsL, 1) i8_large_persistent_kernel(const i8_problem* __restrict__ probs,
+                                                                           const I8Epi* __restrict__ epis,
+                                                                           int* __restrict__ sched) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+  auto pro = [&](const Unit& t) {
+    if (epi_of(epis, t.pi).mode & kEpiPacked) TileSrc<CfgL, true>(probs[t.pi], t.tm, t.tn).prologue(lds);
+    else TileSrc<CfgL, false>(probs[t.pi], t.tm, t.tn).prologue(lds);
+  };
+  persistent<kGroupML, true>(sched, probs, pro, [&](const Unit& t, auto& claim, auto& next) -> bool {
+    return (epi_of(epis, t.pi).mode & kEpiPacked)
+               ? run_tile<CfgL, true, false>(lds, probs, epis, t.pi, t.tm, t.tn, claim, next)
+               : run_tile<CfgL, false, false>(lds, probs, epis, t.pi, t.tm, t.tn, claim, next);
+  });
 }
 
 // ----------------------------------------------------------------------------- host side
@@ -539,6 +756,7 @@ struct Ent {
 };
 std::mutex g_mu;
 std::vector<Ent> g_ents;
+std::vector<int> g_order;
 
 bool valid_problem(const i8_problem& p) {
   if (p.m < 0 || p.n < 0 || p.kp < 0 || (p.kp % 32) != 0 || p.kp > OZ2_MAX_K) return false;
@@ -565,8 +783,13 @@ int auto_cfg(int m, int n) {
 
 }  // namespace
 
+bool i8_env_persistent() {
+  const char* e = std::getenv("GGEMM_I8_SCHED");
+  return e && !std::strcmp(e, "persistent");
+}
+
 int i8_build_schedule(const i8_problem* h, int num, void* h_ws, size_t ws_bytes, i8_sched_info* info, int num_cus,
-                      int large, int* kernel) {
+                      int large, int* kernel, bool persistent) {
   if (num < 0 || (num > 0 && !h) || !h_ws || !info) return 1;
   if (ws_bytes < sched_bytes(num)) return 2;
   if (kernel) *kernel = kI8General;
@@ -608,31 +831,70 @@ int i8_build_schedule(const i8_problem* h, int num, void* h_ws, size_t ws_bytes,
     }
     if (force_large || (all && t >= num_cus)) {
       for (auto& e : ents) {
+        e.cfg = 0;
         e.tiles = ((h[e.prob].m + 255) / 256) * ((h[e.prob].n + 255) / 256);
         e.cost = 256.0 * 256.0 * (double)(h[e.prob].kp + 128);
       }
       if (kernel) *kernel = kI8Large;
     }
   }
+  if (kernel && persistent) *kernel |= kI8Persistent;
+  // longest-processing-time order (heaviest tiles first)
   std::stable_sort(ents.begin(), ents.end(), [](const Ent& a, const Ent& b) {
     if (a.cost != b.cost) return a.cost > b.cost;
     return a.tiles > b.tiles;
   });
-  int* img = static_cast<int*>(h_ws);
+  // Queues of the persistent kernels: chunks of c consecutive tiles of the LPT table dealt
+  // round-robin to the XCDs (c = 32, GGEMM_I8_CHUNK=c overrides; same-box GEMM times at c = 32 vs
+  // whole products per XCD: 121.5 vs 129.2 ms on 8 x 8192^2 x 16384, equal on 1024^3 products), or
+  // with c = 0 whole entries, each in turn onto the least loaded queue (ties: lowest index), every
+  // queue in LPT order.  The hardware-dispatched kernels map workgroups to tiles themselves and
+  // take the table in LPT order.
+  static const int env_chunk = [] {
+    const char* e = std::getenv("GGEMM_I8_CHUNK");
+    return e ? std::max(0, std::atoi(e)) : kChunk;
+  }();
+  const int chunk = persistent ? env_chunk : 1;
   const size_t ne = ents.size();
+  std::vector<int>& order = g_order;
+  order.resize(ne);
+  double load[kXcds] = {};
+  int count[kXcds] = {};
+  std::vector<int> xq(ne);
+  for (size_t j = 0; j < ne; ++j) {
+    int best = 0;
+    for (int x = 1; x < kXcds && chunk == 0; ++x)
+      if (load[x] < load[best]) best = x;
+    xq[j] = best;
+    load[best] += ents[j].cost * ents[j].tiles;
+    ++count[best];
+  }
+  int first[kXcds + 1] = {};
+  for (int x = 0; x < kXcds; ++x) first[x + 1] = first[x] + count[x];
+  {
+    int pos[kXcds];
+    for (int x = 0; x < kXcds; ++x) pos[x] = first[x];
+    for (size_t j = 0; j < ne; ++j) order[pos[xq[j]]++] = (int)j;
+  }
+  int* img = static_cast<int*>(h_ws);
   int* prefix = img + kSchedHdr;
   int* entry = prefix + ne + 1;
-  long long tot = 0;
-  for (size_t j = 0; j < ne; ++j) {
-    prefix[j] = (int)tot;
-    tot += ents[j].tiles;
-    entry[j] = (ents[j].prob << 2) | ents[j].cfg;
-  }
-  prefix[ne] = (int)tot;
-  if (tot > 0x7fffffffLL - 1000000) return 5;
   std::memset(img, 0, sizeof(int) * kSchedHdr);
+  long long tot = 0;
+  for (size_t j = 0, x = 0; j < ne; ++j) {
+    while ((int)x < kXcds && first[x] == (int)j) img[kHdrXcd + x++] = (int)tot;
+    const Ent& e = ents[order[j]];
+    prefix[j] = (int)tot;
+    tot += e.tiles;
+    entry[j] = (e.prob << 2) | e.cfg;
+  }
+  if (tot > 0x7fffffffLL - 1000000) return 5;
+  for (int x = 0; x <= kXcds; ++x)
+    if (first[x] == (int)ne) img[kHdrXcd + x] = (int)tot;
+  prefix[ne] = (int)tot;
   img[0] = (int)tot;
   img[1] = (int)ne;
+  img[3] = persistent ? chunk : 0;
   bool same = ne > 0;
   for (size_t j = 1; j < ne && same; ++j) same = ents[j].tiles == ents[0].tiles;
   img[2] = same ? ents[0].tiles : 0;
@@ -663,7 +925,11 @@ bool lds_attrs_set() {
     if (hipFuncSetAttribute((const void*)i8_grouped_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kSmem) !=
             hipSuccess ||
         hipFuncSetAttribute((const void*)i8_large_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kSmemL) !=
-            hipSuccess)
+            hipSuccess ||
+        hipFuncSetAttribute((const void*)i8_grouped_persistent_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            kSmem) != hipSuccess ||
+        hipFuncSetAttribute((const void*)i8_large_persistent_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            kSmemL) != hipSuccess)
       return false;
     done[dev] = 1;
   }
@@ -677,13 +943,31 @@ int i8_launch(const i8_problem* d_probs, const I8Epi* d_epi, const void* d_sched
   if (info->num_launches == 0 || info->tiles_main == 0) return 0;
   if (!d_probs || !d_sched) return 1;
   if (!lds_attrs_set()) return 6;
-  if (kernel == kI8Large)
+  int* sched = static_cast<int*>(const_cast<void*>(d_sched));
+  const bool large = (kernel & kI8Large) != 0;
+  if (kernel & kI8Persistent) {
+    // persistent workgroups: as many as the compute units hold at once (one 16-wave workgroup or two
+    // 8-wave workgroups per unit), at most one per tile; the schedule image carries the queue
+    // counters the kernel updates.  Same-box GEMM times against one workgroup per tile (the
+    // default): 1.31 vs 1.25 ms on 64 x 1024^3 (16 planes), 2.81 vs 2.53 ms on the ragged group,
+    // 121.5 vs 120.0 ms on 8 x 8192^2 x 16384 -- the dispatcher starts a new workgroup on a freed
+    // slot while the unit's other workgroup computes, which the persistent loop's per-tile handoff
+    // (a workgroup barrier, the counter fetch and the next tile's lookup) does not beat.
+    const DevCtx* c = dev_ctx();
+    if (!c) return 6;
+    const int slots = (large ? 1 : 2) * c->num_cus;
+    const unsigned grid = (unsigned)std::min(info->tiles_main, slots);
+    if (large)
+      hipLaunchKernelGGL(i8_large_persistent_kernel, dim3(grid), dim3(kThreadsL), kSmemL, s, d_probs, d_epi, sched);
+    else
+      hipLaunchKernelGGL(i8_grouped_persistent_kernel, dim3(grid), dim3(kThreads), kSmem, s, d_probs, d_epi, sched);
+  } else if (large) {
     hipLaunchKernelGGL(i8_large_kernel, dim3((unsigned)info->tiles_main), dim3(kThreadsL), kSmemL, s, d_probs, d_epi,
-                       static_cast<const int*>(d_sched));
-
-  else
+                       sched);
+  } else {
     hipLaunchKernelGGL(i8_grouped_kernel, dim3((unsigned)info->tiles_main), dim3(kThreads), kSmem, s, d_probs, d_epi,
-                       static_cast<const int*>(d_sched));
+                       sched);
+  }
   return hipGetLastError() == hipSuccess ? 0 : 6;
 }
 
@@ -698,12 +982,13 @@ extern "C" size_t i8_grouped_gemm_sched_ws_bytes(int max_problems, size_t) {
 extern "C" int i8_grouped_gemm_build_schedule(const i8_problem* h_probs, int num, void* h_ws, size_t ws_bytes,
                                               i8_sched_info* info) {
   DevCtx* c = dev_ctx();
-  return i8_build_schedule(h_probs, num, h_ws, ws_bytes, info, c ? c->num_cus : 256);
+  return i8_build_schedule(h_probs, num, h_ws, ws_bytes, info, c ? c->num_cus : 256, kLargeNever, nullptr,
+                           i8_env_persistent());
 }
 
 extern "C" int i8_grouped_gemm_launch(const i8_problem* d_probs, int, const void* d_sched_ws,
                                       const i8_sched_info* info, hipStream_t s) {
-  return i8_launch(d_probs, nullptr, d_sched_ws, info, s);
+  return i8_launch(d_probs, nullptr, d_sched_ws, info, s, i8_env_persistent() ? kI8Persistent : kI8General);
 }
 
 extern "C" int i8_grouped_gemm_ex(const i8_problem* d_probs, int num, const i8_problem* h_probs, void* d_sched_ws,
@@ -721,7 +1006,7 @@ extern "C" int i8_grouped_gemm_ex(const i8_problem* d_probs, int num, const i8_p
   if (hipMemcpyAsync(d_sched_ws, img.data(), info.bytes_used, hipMemcpyHostToDevice, s) != hipSuccess) return 7;
   // the pageable source must stay valid until the copy has consumed it
   if (hipStreamSynchronize(s) != hipSuccess) return 7;
-  rc = i8_launch(d_probs, nullptr, d_sched_ws, &info, s);
+  rc = i8_launch(d_probs, nullptr, d_sched_ws, &info, s, i8_env_persistent() ? kI8Persistent : kI8General);
   if (!rc && num_launches) *num_launches = info.num_launches;
   return rc;
 }

@@ -153,3 +153,44 @@ def test_plan_update_pointers_long_k_matches_oracle():
     finally:
         G.lib().ggemm_destroy_plan(plan)
         h.close()
+
+
+def test_persistent_plan_replays_match_oracle():
+    """A plan captured with the persistent work-stealing INT8 kernel (GGEMM_I8_SCHED=persistent at
+    handle creation) replayed four times, alternating two data sets, with eager work between the
+    replays: the queue counters live in the plan's schedule image and reset themselves, so every
+    replay is bitwise equal to the oracle (COUNT mode)."""
+    import os
+    shapes = [(300, 260, 700)] * 3 + [(96, 130, 2000), (520, 64, 90)]
+    X = Case(shapes, 71, phi=1.0, beta=0.5)
+    Y = Case(shapes, 72, phi=1.0, beta=0.5)
+    cfg = G.Config(0, 1e-15, 0, G.REPAIR_COUNT)
+    rc, plan_o = oracle_plan(X, cfg, G.PATH_EMU_GROUPED)
+    assert rc == 0
+    saved = dict(os.environ)
+    os.environ["GGEMM_I8_SCHED"] = "persistent"
+    try:
+        h = G.Handle(len(shapes), *[max(a, b) for a, b in zip(X.sizes(), Y.sizes())])
+    finally:
+        os.environ.clear()
+        os.environ.update(saved)
+    arr = G.problems_array(X.problems())
+    err = C.c_int(0)
+    plan = G.lib().ggemm_make_plan_ex(h.h, G.PATH_EMU_GROUPED, C.byref(cfg), arr, len(shapes), C.byref(err))
+    assert plan, err.value
+    ptr = lambda ts: (C.c_void_p * len(shapes))(*[t.data_ptr() for t in ts])
+    try:
+        for rep in range(4):
+            case = X if rep % 2 == 0 else Y
+            case.reset_C()
+            assert G.lib().ggemm_plan_update_pointers(plan, ptr(case.dA), ptr(case.dB), ptr(case.dC)) == 0
+            say(f"persistent plan replay {rep}")
+            assert G.lib().ggemm_execute_plan(plan, None) == 0
+            torch.cuda.synchronize()
+            torch.zeros(1 << 20, device="cuda").sum().item()   # eager work between replays
+            for g, (hp, e) in enumerate(zip(case.hp, plan_o)):
+                Co, _ = hp.emulate(O.REPAIR_COUNT, e.num_moduli)
+                assert same_bits(case.C(g), Co), f"replay {rep}: problem {g} differs"
+    finally:
+        G.lib().ggemm_destroy_plan(plan)
+        h.close()

@@ -234,19 +234,44 @@ def run_kernel(case, kernel, cfg=CFG_EMU, **env):
         rc, st = run(case, G.PATH_EMU_GROUPED, cfg, handle=h)
         assert rc == 0
         want = {"large": "i8_large_kernel", "general": "i8_grouped_kernel"}[kernel]
+        if env.get("GGEMM_I8_SCHED") == "persistent":
+            want = want.replace("_kernel", "_persistent_kernel")
         assert G.lib().ggemm_profile_i8_kernel().decode() == want
         check_case(case, G.PATH_EMU_GROUPED, cfg, st, O.REPAIR_COUNT)
         return [case.C(g).copy() for g in range(len(case.hp))]
 
 
+@pytest.mark.parametrize("sched", ["dispatch", "persistent"])
 @pytest.mark.parametrize("kernel", ["large", "general"])
-def test_large_tile_kernel_ragged_edges(kernel):
+def test_large_tile_kernel_ragged_edges(kernel, sched):
     """The large-tile INT8 kernel (forced with GGEMM_I8_KERNEL; by default it serves long-k
-    calls) and the general kernel on the same products: m, n are not multiples of 256 (clamped
-    edge rows) and kp = 480 is 32 mod 64 (the zeroed half stage)."""
+    calls) and the general kernel on the same products, each with one workgroup per tile and as
+    persistent work-stealing kernels (GGEMM_I8_SCHED=persistent): m, n are not multiples of 256
+    (clamped edge rows) and kp = 480 is 32 mod 64 (the zeroed half stage)."""
     case = Case([(520, 600, 470)] * 3, 20261206, phi=0.5, beta=0.5)
-    say(f"{kernel} kernel, ragged edges")
-    run_kernel(case, kernel)
+    say(f"{kernel} kernel, ragged edges, {sched}")
+    run_kernel(case, kernel, **({"GGEMM_I8_SCHED": "persistent"} if sched == "persistent" else {}))
+
+
+@pytest.mark.parametrize("kernel", ["large", "general"])
+def test_persistent_kernels_ragged_group(kernel):
+    """The persistent work-stealing INT8 kernels on a ragged group: tile configurations change
+    between consecutive tiles of a workgroup (general kernel), queues run dry at different times and
+    workgroups steal; k from 32 to 1055, half stages included.  Oracle bits and counters in COUNT
+    mode, twice on one handle (the queue counters reset themselves)."""
+    rng = np.random.default_rng(20261215)
+    shapes = [(int(rng.integers(1, 700)), int(rng.integers(1, 700)), int(rng.integers(32, 1056))) for _ in range(40)]
+    case = Case(shapes, 20261215, phi=1.0, beta=0.5)
+    say(f"persistent {kernel} kernel, ragged group of {len(shapes)}")
+    env = {"GGEMM_I8_SCHED": "persistent"}
+    with kernel_handle(case, kernel, **env) as h:
+        for rep in range(2):
+            case.reset_C()
+            rc, st = run(case, G.PATH_EMU_GROUPED, CFG_EMU, handle=h)
+            assert rc == 0, rep
+            want = {"large": "i8_large_persistent_kernel", "general": "i8_grouped_persistent_kernel"}[kernel]
+            assert G.lib().ggemm_profile_i8_kernel().decode() == want
+            check_case(case, G.PATH_EMU_GROUPED, CFG_EMU, st, O.REPAIR_COUNT)
 
 
 @pytest.mark.parametrize("colmajor", [False, True])

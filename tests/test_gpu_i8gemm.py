@@ -78,19 +78,30 @@ def test_float64_checker_is_exact():
         assert np.array_equal(ref.astype(np.float64), f)
 
 
+@pytest.fixture(params=["dispatch", "persistent"])
+def sched(request, monkeypatch):
+    """The kernel-level API runs one workgroup per tile, or (GGEMM_I8_SCHED=persistent) the persistent
+    work-stealing kernels."""
+    if request.param == "persistent":
+        monkeypatch.setenv("GGEMM_I8_SCHED", "persistent")
+    else:
+        monkeypatch.delenv("GGEMM_I8_SCHED", raising=False)
+    return request.param
+
+
 @pytest.mark.parametrize("cfg", [0, 1, 2, -1, "mixed"])
-def test_hetero_bit_exact(cfg):
+def test_hetero_bit_exact(cfg, sched):
     g = Group(HETERO, 1234)
-    say(f"i8 hetero cfg={cfg}")
+    say(f"i8 hetero cfg={cfg} {sched}")
     nl, Cres = g.run((lambda i: i % 3) if cfg == "mixed" else cfg)
     assert nl == 1
     g.check(Cres)
 
 
-def test_int32_edge_all_minus128():
+def test_int32_edge_all_minus128(sched):
     g = Group([(3, 5, 131040), (17, 9, 131040), (1, 1, 32)], 1, fill=-128)
     for cfg in (-1, 0, 2):
-        say(f"i8 -128 edge cfg={cfg}")
+        say(f"i8 -128 edge cfg={cfg} {sched}")
         nl, Cres = g.run(cfg)
         for i, (m, n, kp) in enumerate(g.shapes):
             got = Cres[g.offC[i]:g.offC[i] + m * n]
@@ -98,9 +109,11 @@ def test_int32_edge_all_minus128():
     assert 16384 * 131040 == 2146959360
 
 
-def test_relaunch_split_schedule():
-    """build_schedule + launch twice without re-uploading the schedule."""
-    g = Group([(200, 100, 640), (64, 300, 96), (5, 5, 32)], 99)
+def test_relaunch_split_schedule(sched):
+    """build_schedule + launch three times without re-uploading the schedule (the persistent kernels'
+    queue counters reset themselves at the end of each launch)."""
+    say(f"i8 relaunch {sched}")
+    g = Group([(200, 100, 640), (64, 300, 96), (5, 5, 32)] + [(512, 384, 256)] * 40, 99)
     probs = g.problems(-1)
     d_probs = dev_struct_array(probs, G.I8Problem)
     nb = G.lib().i8_grouped_gemm_sched_ws_bytes(len(probs), 0)
@@ -110,10 +123,12 @@ def test_relaunch_split_schedule():
     assert G.lib().i8_grouped_gemm_build_schedule(arr, len(probs), himg, nb, C.byref(info)) == 0
     assert info.num_launches == 1 and info.bytes_used <= nb
     ws = dev(np.frombuffer(bytes(himg), dtype=np.uint8))
-    for _ in range(2):
+    for _ in range(3):
         g.dC.zero_()
         assert G.lib().i8_grouped_gemm_launch(d_probs.data_ptr(), len(probs), ws.data_ptr(), C.byref(info), None) == 0
         g.check(host(g.dC))
+    # counters and finished count back at zero after every launch
+    assert not host(ws).view(np.int32)[32:41].any()
 
 
 def test_invalid_problem_rejected():
