@@ -44,7 +44,7 @@ FP64_PEAK = 78.6e12    # MI355X dense FP64 MFMA, flop / s
 STAGES = ("prep", "i8_gemm", "reconstruct", "native", "memops")
 _STAGE_RE = [
     (re.compile(r"\bprep_kernel\b"), "prep"),
-    (re.compile(r"\bi8_(grouped|large)_kernel\b"), "i8_gemm"),
+    (re.compile(r"\bi8_(grouped|large)(_persistent)?_kernel\b"), "i8_gemm"),
     (re.compile(r"\brecon_kernel\b"), "reconstruct"),
     (re.compile(r"\bf64_\w*kernel\b"), "native"),
     (re.compile(r"copyBuffer|fillBuffer|__amd_rocclr"), "memops"),

@@ -30,6 +30,7 @@ struct GroupedCall {
   bool blocked = false;           // digit and abs planes in the blocked layout
   bool packed = false;            // residue planes in the packed layout
   int f64_tiles = 0;              // native GEMM launch word (tile count, kF64Tile128 for 128 x 128 tiles)
+  ReconGrid rgrid{};              // compact reconstruct / dot-product grids
   size_t h2d_bytes = 0;           // bytes of the blob to copy
 };
 

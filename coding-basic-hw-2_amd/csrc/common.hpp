@@ -151,11 +151,26 @@ int i8_launch(const i8_problem* d_probs, const I8Epi* d_epi, const void* d_sched
 // Where the reconstruct reads a problem's plane products in the production pipeline: CRT digits
 // y_l (one byte per entry, plane l at Y + l * y_stride) and the abs-plane product L (int32), both
 // column-major with ld m, or both blocked (layout above) when the call's descriptors say so.
+// F (blocked layout only): per 16 x 16 block (blocked order) four 64-bit words, bit l of word e set
+// when entry e of MFMA lane l of the block takes an FP64 dot product; written by the reconstruct for
+// every block of the problem, read by the dot-product pass.
+// t0 / d0: the problem's first tile in the grouped call's compact reconstruct / dot-product grid (the
+// tiles of all problems back to back, so no workgroup of the grid lies outside its problem).
 struct YDesc {
   const uint8_t* Y;
   size_t y_stride;
   const int32_t* L;
+  uint64_t* F;
+  int t0, d0;
 };
+// Compact grids of a grouped call (ne problems): tiles in all and, when every problem has the same
+// count, that count (else 0) -- for the reconstruct and for the dot-product pass.
+struct ReconGrid {
+  int ne, tiles, per, dtiles, dper;
+};
+// Reconstruct tile shapes (rows x columns per workgroup): blocked digits / column-major, and the
+// dot-product pass's tile
+constexpr int kReconTileMB = 64, kReconTileNB = 16, kReconTileMC = 128, kReconTileNC = 8, kDotTile = 64;
 
 // FP64 MFMA grouped GEMM (native routes).  h_ws receives the schedule image; *launch receives the
 // launch word for f64_launch: the tile count in bits 0-29, kF64Tile128 set for 128 x 128 tiles (0:
@@ -173,9 +188,13 @@ int f64_launch(const F64Problem* d_probs, const void* d_sched, int launch, hipSt
 int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t s, int fold_q, int packed,
                 int max_moduli);
 // yd == nullptr: read the int32 planes of oz2_problem::C32 (kernel-level API); else the digits.
-// blocked: the digits and L of every problem are in the blocked layout (production, yd != nullptr)
+// blocked: the digits and L of every problem are in the blocked layout (production, yd != nullptr);
+// the reconstruct then flags the entries that take FP64 dot products and a second kernel computes
+// them.  *launches (if given) receives the number of kernels launched.
+// grid (production calls): the compact grids of the yd[].t0 / d0 offsets; nullptr: one grid row per
+// problem, as wide as the largest problem's tile count (kernel-level API, per-problem launches).
 int recon_launch(const oz2_problem* d, const YDesc* yd, int num, int max_m, int max_n, hipStream_t s, int mode,
-                 bool blocked = false);
+                 bool blocked = false, int* launches = nullptr, const ReconGrid* grid = nullptr);
 
 }  // namespace ggemm
 

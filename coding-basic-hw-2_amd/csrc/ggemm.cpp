@@ -3,8 +3,10 @@
 // Mirrors the reference's orchestration semantics (src/ggemm.cu): all device workspace and host
 // scratch are allocated in ggemm_create_ex; a call validates, plans, writes every descriptor into
 // a double-buffered pinned slot, issues ONE H2D of the used part of the blob and then the
-// kernels: prep -> grouped INT8 GEMM -> reconstruct (3 launches for any group size) plus one
-// grouped native FP64 GEMM launch when some problems take a native route.
+// kernels: prep -> grouped INT8 GEMM -> reconstruct -> FP64 dot products of the entries the
+// reconstruct flagged (4 launches for any group size; 3 when the digits are column-major, where the
+// reconstruct computes them itself) plus one grouped native FP64 GEMM launch when some problems
+// take a native route.
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
@@ -220,14 +222,16 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
   // product workspace (the C32 buffer): CRT digit planes [plane < nmax][problem] of SY bytes
   // each, then the int32 abs-plane products.  Column-major fits because nmax SY + 4 SC <=
   // pmax 4 SC; the blocked layout (whole 16 x 16 blocks) is used when its padded planes fit too.
-  size_t SY = 0, SYb = 0, SLb = 0;
+  // The blocked layout also keeps the dot-product flags (32 bytes per 16 x 16 block) after the L planes.
+  size_t SY = 0, SYb = 0, SLb = 0, SFb = 0;
   for (int j = 0; j < c.ne; ++j) {
     const ggemm_problem_t& p = probs[emu_idx[j]];
     SY += align_up((size_t)p.m * p.n, kBufAlign);
     SYb += align_up(blocked_plane_entries(p.m, p.n), kBufAlign);
     SLb += align_up(blocked_plane_entries(p.m, p.n), kBufAlign / 4) * sizeof(int32_t);
+    SFb += align_up(blocked_plane_entries(p.m, p.n) / 8, kBufAlign);
   }
-  c.blocked = !h->digits_colmajor && (size_t)nmax * SYb + SLb <= h->C32_bytes;
+  c.blocked = !h->digits_colmajor && (size_t)nmax * SYb + SLb + SFb <= h->C32_bytes;
   // Packed residue planes make every 64-byte k-stage of a tile's rows contiguous, which the INT8
   // GEMM's operand stream prefers at moderate k (measured: 1024^3 products 14 % faster together
   // with the blocked digits); at k = 16384 the row-major planes stream better (5 % slower packed).
@@ -237,7 +241,8 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
   if (c.blocked) SY = SYb;
   uint8_t* ybase = reinterpret_cast<uint8_t*>(h->C32);
   int32_t* lbase = reinterpret_cast<int32_t*>(ybase + (size_t)nmax * SY);
-  size_t oa = 0, ob = 0, orow = 0, ocol = 0, q = 0, oy = 0, ol = 0;
+  uint8_t* fbase = reinterpret_cast<uint8_t*>(lbase) + SLb;
+  size_t oa = 0, ob = 0, orow = 0, ocol = 0, q = 0, oy = 0, ol = 0, of = 0;
   for (int j = 0; j < c.ne; ++j) {
     const int g = emu_idx[j];
     const ggemm_problem_t& p = probs[g];
@@ -264,6 +269,21 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
     yd.Y = ybase + oy;
     yd.y_stride = SY;
     yd.L = lbase + ol;
+    yd.F = c.blocked ? reinterpret_cast<uint64_t*>(fbase + of) : nullptr;
+    {   // compact reconstruct / dot-product grids
+      const int rm = c.blocked ? kReconTileMB : kReconTileMC, rn = c.blocked ? kReconTileNB : kReconTileNC;
+      const long long rt = (long long)((p.m + rm - 1) / rm) * ((p.n + rn - 1) / rn);
+      const long long dt = c.blocked ? (long long)((p.m + kDotTile - 1) / kDotTile) * ((p.n + kDotTile - 1) / kDotTile) : 0;
+      ReconGrid& rg = c.rgrid;
+      if (rg.tiles + rt > 0x7fffffffLL || rg.dtiles + dt > 0x7fffffffLL) return GGEMM_ERR_INVALID;
+      yd.t0 = rg.tiles;
+      yd.d0 = rg.dtiles;
+      rg.per = j == 0 ? (int)rt : (rg.per == (int)rt ? rg.per : 0);
+      rg.dper = j == 0 ? (int)dt : (rg.dper == (int)dt ? rg.dper : 0);
+      rg.tiles += (int)rt;
+      rg.dtiles += (int)dt;
+      rg.ne = j + 1;
+    }
     o.C32 = lbase + ol; o.c32_mod_stride = 0;   // the reconstruct reads yd, not C32
     const int N = e.num_moduli;
     for (int l = 0; l <= N; ++l, ++q) {
@@ -284,6 +304,7 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
     const size_t plane = c.blocked ? blocked_plane_entries(p.m, p.n) : (size_t)p.m * p.n;
     oy += align_up(plane, kBufAlign);
     ol += align_up(plane, kBufAlign / 4);
+    of += align_up(blocked_plane_entries(p.m, p.n) / 8, kBufAlign);
     oa += align_up((size_t)p.m * kp, kBufAlign);
     ob += align_up((size_t)p.n * kp, kBufAlign);
     orow += align_up((size_t)OZ2_ROW_WS_PER_ROW * p.m, 64);
@@ -344,8 +365,9 @@ int enqueue_grouped(const GroupedCall& c, const char* db, hipStream_t s, int rep
     *launches += c.i8info.num_launches;
     prof::last_i8 = c.i8_kernel;
     prof::mark(prof_set, 2, s);
-    if (recon_launch(doz, dyd, c.ne, c.max_m, c.max_n, s, repair, c.blocked)) return GGEMM_ERR_NUMERICS;
-    ++*launches;
+    int nr = 0;
+    if (recon_launch(doz, dyd, c.ne, c.max_m, c.max_n, s, repair, c.blocked, &nr, &c.rgrid)) return GGEMM_ERR_NUMERICS;
+    *launches += nr;
     prof::mark(prof_set, 3, s);
   } else {
     prof::mark(prof_set, 1, s);
@@ -524,11 +546,12 @@ int path_emu_loop(ggemm_handle_t h, bool batched, const ggemm_problem_t* probs, 
       if (r) break;
     }
     q += planes;
-    if (recon_launch(doz + j, dyd + j, 1, hoz[j].m, hoz[j].n, h->stream, repair, c.blocked)) {
+    int nr = 0;
+    if (recon_launch(doz + j, dyd + j, 1, hoz[j].m, hoz[j].n, h->stream, repair, c.blocked, &nr)) {
       r = GGEMM_ERR_NUMERICS;
       break;
     }
-    ++nl;
+    nl += nr;
   }
   if (!r && c.nn > 0 && c.f64_tiles > 0) {
     if (f64_launch(reinterpret_cast<const F64Problem*>(db + c.L.off_f64), db + c.L.off_sf64, c.f64_tiles, h->stream))

@@ -252,21 +252,48 @@ __device__ __forceinline__ void tile_dots(const oz2_problem& pr, int r0, int cb,
   }
 }
 
+// The workgroup's problem and tile inside it.  ne > 0: compact grid (workgroup blockIdx.x of the
+// tiles of all problems back to back; per > 0: every problem has per tiles, else the problem is the
+// last one whose first tile, yds[p].t0 or .d0, is at most blockIdx.x); ne == 0: problem blockIdx.y,
+// tile blockIdx.x.
+template <bool kDots>
+__device__ __forceinline__ void grid_tile(const YDesc* __restrict__ yds, int ne, int per, int& p, int& lt) {
+  const int g = blockIdx.x;
+  if (ne == 0) {
+    p = blockIdx.y;
+    lt = g;
+  } else if (per > 0) {
+    p = g / per;
+    lt = g - p * per;
+  } else {
+    int lo = 0, hi = ne - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if ((kDots ? yds[mid].d0 : yds[mid].t0) <= g) lo = mid; else hi = mid - 1;
+    }
+    p = lo;
+    lt = g - (kDots ? yds[lo].d0 : yds[lo].t0);
+  }
+}
+
 template <bool kDigits, bool kBlocked>
 __global__ void __launch_bounds__(kThreads) recon_kernel(const oz2_problem* __restrict__ probs,
                                                          const YDesc* __restrict__ yds, int mode,
                                                          const CrtTables* __restrict__ tab,
-                                                         unsigned long long* __restrict__ cnt) {
+                                                         unsigned long long* __restrict__ cnt, int gne, int gper) {
   __shared__ unsigned long long red[3][kThreads / 64];
-  const oz2_problem& pr = probs[blockIdx.y];
+  int pi, lt;
+  grid_tile<false>(yds, gne, gper, pi, lt);
+  const oz2_problem& pr = probs[pi];
   const int N = pr.num_moduli;
   const int m = pr.m, n = pr.n, K = pr.k;
   Counts cn{0u, 0u, 0u};
   constexpr int RM = kBlocked ? kBTileM : kTileM, CN = kBlocked ? kBTileN : kTileN;   // tile rows, columns
-  // dot products' k-chunks: per wave (blocked layout) or for the whole tile
-  __shared__ double tA[kBlocked ? 4 * 16 * kKC : kKC * RM], tB[kBlocked ? 4 * 16 * (kKC + 1) : CN * (kKC + 1)];
+  // dot products' k-chunks for the whole tile (column-major; the blocked layout leaves its dot
+  // products to dots_kernel)
+  __shared__ double tA[kBlocked ? 2 : kKC * RM], tB[kBlocked ? 2 : CN * (kKC + 1)];
   const int tiles_m = (m + RM - 1) / RM;
-  const int r0 = ((int)blockIdx.x % max(tiles_m, 1)) * RM, cb = ((int)blockIdx.x / max(tiles_m, 1)) * CN;
+  const int r0 = (lt % max(tiles_m, 1)) * RM, cb = (lt / max(tiles_m, 1)) * CN;
   int lr, lc;   // the thread's rows lr .. lr + 3 and column lc inside the tile
   if (kBlocked) {   // a wave per 16 x 16 block, lane = the block's MFMA lane: 4 rows of one column
     const int lane = threadIdx.x & 63;
@@ -321,7 +348,7 @@ __global__ void __launch_bounds__(kThreads) recon_kernel(const oz2_problem* __re
       // blocked: the 4-entry word always exists (entries past m are padding, never used)
       const size_t off = kBlocked ? blocked_word(i0, j, (m + 15) / 16) : (size_t)i0 + (size_t)j * m;
       if (kDigits) {
-        const YDesc yd = yds[blockIdx.y];
+        const YDesc yd = yds[pi];
         const GLOBAL uint8_t* Y = gp(yd.Y) + off;
 #pragma unroll
         for (int l = 0; l < kMaxModuli; ++l) {
@@ -407,16 +434,17 @@ __global__ void __launch_bounds__(kThreads) recon_kernel(const oz2_problem* __re
   // when few lanes need them, else a whole block / tile at once through LDS k-chunks (every lane
   // helps; values identical, since each entry is still one fma chain in ascending k).  Blocked
   // layout: per wave, without a workgroup barrier; column-major: per workgroup.
-  bool many;
+  bool many = false;
   if (kBlocked) {
-    many = __popcll(__ballot(dmask != 0u)) >= kWaveDots;
-    if (many) {
-      const int w = threadIdx.x >> 6;
-      double acc[4];
-      wave_dots(pr, r0 + 16 * w, cb, threadIdx.x & 63, tA + w * 16 * kKC, tB + w * 16 * (kKC + 1), acc);
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if ((dmask >> e) & 1u) cp[e] = from_dot(alpha, beta, acc[e], beta != 0.0 ? cp[e] : 0.0);
+    // the wave's block: flag words instead of dot products (the dot-product pass computes them);
+    // written for every block of the problem, so no stale flag survives from an earlier call
+    const uint64_t f0 = __ballot(dmask & 1u), f1 = __ballot((dmask >> 1) & 1u);
+    const uint64_t f2 = __ballot((dmask >> 2) & 1u), f3 = __ballot((dmask >> 3) & 1u);
+    const int br = r0 + 16 * (int)(threadIdx.x >> 6);
+    if ((threadIdx.x & 63) == 0 && N >= 1 && N <= kMaxModuli && br < m && cb < n) {
+      const size_t bidx = (size_t)(cb >> 4) * (size_t)((m + 15) >> 4) + (size_t)(br >> 4);
+      GLOBAL uint64_t* F = gpw(yds[pi].F) + 4 * bidx;
+      F[0] = f0; F[1] = f1; F[2] = f2; F[3] = f3;
     }
   } else {
     many = __syncthreads_count(dmask != 0u) >= kTileDots;
@@ -428,7 +456,7 @@ __global__ void __launch_bounds__(kThreads) recon_kernel(const oz2_problem* __re
         if ((dmask >> e) & 1u) cp[e] = from_dot(alpha, beta, acc[e], beta != 0.0 ? cp[e] : 0.0);
     }
   }
-  if (!many && dmask) {
+  if (!kBlocked && !many && dmask) {
     for (int e = 0; e < ne; ++e)
       if ((dmask >> e) & 1u) cp[e] = from_dot(alpha, beta, fp64_dot(pr, i0 + e, j), beta != 0.0 ? cp[e] : 0.0);
   }
@@ -450,10 +478,257 @@ __global__ void __launch_bounds__(kThreads) recon_kernel(const oz2_problem* __re
   }
 }
 
+// ---------------------------------------------------------------- dot-product pass (blocked layout)
+// The production reconstruct (blocked layout) computes no FP64 dot product: it leaves C0 in C for
+// the entries that take one (safety fallback for rows / columns with NaN / Inf, repair of
+// uncertified entries) and flags them, one bit per entry.  dots_kernel then covers a 64 x 64 tile of
+// one problem per workgroup: a tile without flags returns after reading its 512 flag bytes;
+// otherwise every flagged entry's dot product is one sequential fma chain over k in ascending order
+// from 0, as the reference's fp64_dot, whichever of three forms computes it:
+//   * dense: when at least a quarter of the tile's entries are flagged, the workgroup computes all 4096
+//     chains of the tile at once, each thread a 4 x 4 register block (16 chains), the k-chunks of
+//     A (64 rows) and B (64 columns) double-buffered in LDS and read as 32-byte row / column
+//     quads that a wave's lanes share (broadcast reads): 4 LDS reads per 16 fmas;
+//   * per block: a block with flagged entries in at least kWaveDots lanes takes them all with 4
+//     chains per lane (wave_dots: wave w the blocks of block column w);
+//   * sparse: the remaining entries go to a per-workgroup list; for up to 16 entries at a time
+//     all 256 threads stage their A rows and B columns through LDS in k-chunks of 64 to 1024 (all
+//     of a chunk's loads in flight together, the next chunk's while the chains run), one lane per
+//     chain -- instead of one lane loading its A row, lda apart, and its B column itself.
+constexpr int kRT = 64;            // tile rows and columns
+constexpr int kDenseMin = 1024;    // flagged entries of a tile from which it takes the dense form
+constexpr int kDK = 8;             // dense k-chunk
+constexpr int kSG = 16;            // sparse: entries per group
+constexpr int kListCap = 256;      // sparse list capacity (16 blocks x 3 lanes x 4 entries fit)
+constexpr int kWaveLds = 16 * kKC + 16 * (kKC + 1);   // doubles of one wave's wave_dots staging
+constexpr int kUnion = 4 * kWaveLds;                  // wave_dots x 4 waves; >= dense, sparse
+static_assert(4 * kDK * kRT <= kUnion && 2 * 1024 <= kUnion, "dot-pass LDS union");
+
+__device__ __forceinline__ void lds_sync() { __syncthreads(); }
+
+// flag of tile entry (il, jl): block b = 4 (jl / 16) + il / 16, word il % 4, bit = MFMA lane
+// 16 ((il % 16) / 4) + jl % 16
+__device__ __forceinline__ bool tile_flag(const uint64_t* fl, int il, int jl) {
+  return (fl[4 * (4 * (jl >> 4) + (il >> 4)) + (il & 3)] >> (16 * ((il & 15) >> 2) + (jl & 15))) & 1u;
+}
+
+// All 4096 chains of the tile (rows r0 .., columns c0 ..); thread t: tr = 4 (t / 64) + (t % 64) / 16,
+// tc = t % 16 owns rows 4 tr .. 4 tr + 3 and columns 4 tc .. 4 tc + 3 of the tile.  The flagged
+// entries (fl) are stored: C = alpha d (+ beta C0).
+__device__ __forceinline__ void dense_dots(const oz2_problem& pr, int r0, int c0, const uint64_t* fl, double* buf) {
+  const GLOBAL double* A = gp(pr.A);
+  const GLOBAL double* B = gp(pr.B);
+  const size_t lda = (size_t)pr.lda, ldb = (size_t)pr.ldb;
+  const int m = pr.m, n = pr.n, K = pr.k;
+  const int t = threadIdx.x;
+  const int tr = 4 * (t >> 6) + ((t & 63) >> 4), tc = t & 15;
+  double* sA = buf;                  // [2][kDK][64]: A chunk, rows contiguous
+  double* sB = buf + 2 * kDK * kRT;  // [2][kDK][64]: B chunk, columns contiguous
+  double acc[4][4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) acc[a][b] = 0.0;
+  // staging: A element x = t + 256 s (kk = x / 64, row = x % 64), B element x (col = x / kDK,
+  // kk = x % kDK), NS of each per thread, from clamped (always valid) addresses; rows / columns past
+  // the problem feed entries never stored, k past K is never read by the chains
+  constexpr int NS = kDK * kRT / kThreads;
+  static_assert(NS * kThreads == kDK * kRT, "dense staging split");
+  double va[NS], vb[NS];
+  auto fetch = [&](int kc) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const int x = t + kThreads * s;
+      va[s] = A[(size_t)min(r0 + x % kRT, m - 1) + (size_t)min(kc + x / kRT, K - 1) * lda];
+      vb[s] = B[(size_t)min(kc + x % kDK, K - 1) + (size_t)min(c0 + x / kDK, n - 1) * ldb];
+    }
+  };
+  auto put = [&](int slot) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const int x = t + kThreads * s;
+      sA[slot * kDK * kRT + x] = va[s];                                  // [kk][row], x = 64 kk + row
+      sB[slot * kDK * kRT + (x % kDK) * kRT + x / kDK] = vb[s];          // [kk][col]
+    }
+  };
+  if (K > 0) {
+    fetch(0);
+    put(0);
+  }
+  lds_sync();
+  int slot = 0;
+  for (int kc = 0; kc < K; kc += kDK) {
+    const int kn = min(kDK, K - kc);
+    const bool more = kc + kDK < K;
+    if (more) fetch(kc + kDK);   // the next chunk's loads in flight while this chunk's fmas run
+    const double* a_ = sA + slot * kDK * kRT + 4 * tr;
+    const double* b_ = sB + slot * kDK * kRT + 4 * tc;
+#pragma unroll 2
+    for (int kk = 0; kk < kn; ++kk) {
+      const v2d a01 = *reinterpret_cast<const v2d*>(a_ + kk * kRT);
+      const v2d a23 = *reinterpret_cast<const v2d*>(a_ + kk * kRT + 2);
+      const v2d b01 = *reinterpret_cast<const v2d*>(b_ + kk * kRT);
+      const v2d b23 = *reinterpret_cast<const v2d*>(b_ + kk * kRT + 2);
+      const double av[4] = {a01.x, a01.y, a23.x, a23.y}, bv[4] = {b01.x, b01.y, b23.x, b23.y};
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = fma(av[a], bv[b], acc[a][b]);
+    }
+    if (more) put(slot ^ 1);   // the other slot: every thread finished reading it before the last barrier
+    lds_sync();
+    slot ^= 1;
+  }
+  const double alpha = pr.alpha, beta = pr.beta;
+  GLOBAL double* const C = gpw(pr.C);
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const int jl = 4 * tc + b, j = c0 + jl;
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      const int il = 4 * tr + a, i = r0 + il;
+      if (i < m && j < n && tile_flag(fl, il, jl)) {
+        GLOBAL double* cp = C + i + (size_t)j * pr.ldc;
+        *cp = from_dot(alpha, beta, acc[a][b], beta != 0.0 ? *cp : 0.0);
+      }
+    }
+  }
+}
+
+// The listed entries (tile-local row / column, packed 16 + 16 bits) in groups of at most kSG: lane e
+// of the group runs entry e's chain; all threads stage the group's A rows and B columns through LDS
+// in k-chunks of 1024 / (group size rounded up to a power of two) -- 4 loads of A and 4 of B per
+// thread and chunk, the next chunk's in flight while the chains run on this one.
+__device__ __forceinline__ void sparse_dots(const oz2_problem& pr, int r0, int c0, const uint32_t* list, int L,
+                                            double* buf) {
+  const GLOBAL double* A = gp(pr.A);
+  const GLOBAL double* B = gp(pr.B);
+  const size_t lda = (size_t)pr.lda, ldb = (size_t)pr.ldb;
+  const int K = pr.k;
+  const int t = threadIdx.x;
+  double* sA = buf;          // [group entry][chunk]
+  double* sB = buf + 1024;   // [group entry][chunk]
+  for (int g0 = 0; g0 < L; g0 += kSG) {
+    const int gl = min(kSG, L - g0);
+    const int lg = 32 - __clz(gl - 1);   // ceil(log2 gl): gl <= 1 << lg
+    const int ch = 1024 >> lg;           // k-chunk
+    // staging element x = t + 256 s: entry x >> (10 - lg), kk = x & (ch - 1); entries >= gl load a
+    // clamped copy of the last one (never read)
+    double va[4], vb[4];
+    auto fetch = [&](int kc) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int x = t + 256 * s;
+        const int e = min(x >> (10 - lg), gl - 1), kk = min(kc + (x & (ch - 1)), K - 1);
+        const uint32_t w = list[g0 + e];
+        va[s] = A[(size_t)(r0 + (int)(w & 0xffffu)) + (size_t)kk * lda];
+        vb[s] = B[(size_t)kk + (size_t)(c0 + (int)(w >> 16)) * ldb];
+      }
+    };
+    auto put = [&]() {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        sA[t + 256 * s] = va[s];
+        sB[t + 256 * s] = vb[s];
+      }
+    };
+    double acc = 0.0;
+    if (K > 0) {
+      fetch(0);
+      put();
+    }
+    lds_sync();
+    for (int kc = 0; kc < K; kc += ch) {
+      const int kn = min(ch, K - kc);
+      const bool more = kc + ch < K;
+      if (more) fetch(kc + ch);   // in flight while the chains run
+      if (t < gl) {
+        const double* a_ = sA + t * ch;
+        const double* b_ = sB + t * ch;
+        for (int kk = 0; kk < kn; ++kk) acc = fma(a_[kk], b_[kk], acc);
+      }
+      lds_sync();   // every chain done with this chunk
+      if (more) {
+        put();
+        lds_sync();
+      }
+    }
+    if (t < gl) {
+      const uint32_t w = list[g0 + t];
+      GLOBAL double* cp = gpw(pr.C) + (size_t)(r0 + (int)(w & 0xffffu)) + (size_t)(c0 + (int)(w >> 16)) * pr.ldc;
+      *cp = from_dot(pr.alpha, pr.beta, acc, pr.beta != 0.0 ? *cp : 0.0);
+    }
+    lds_sync();   // the next group's staging overwrites this group's chunk
+  }
+}
+
+__global__ void __launch_bounds__(kThreads) dots_kernel(const oz2_problem* __restrict__ probs,
+                                                        const YDesc* __restrict__ yds, int gne, int gper) {
+  __shared__ __attribute__((aligned(16))) double buf[kUnion];
+  __shared__ uint64_t fl[64];       // flag words of the tile's 16 blocks (4 per block, column-major blocks)
+  __shared__ uint32_t list[kListCap];
+  __shared__ int cnt[2];            // flagged entries of the tile, listed entries
+  int pi, lt;
+  grid_tile<true>(yds, gne, gper, pi, lt);
+  const oz2_problem& pr = probs[pi];
+  const int N = pr.num_moduli;
+  const int m = pr.m, n = pr.n;
+  const int tiles_m = (m + kRT - 1) / kRT;
+  const int r0 = (lt % max(tiles_m, 1)) * kRT, c0 = (lt / max(tiles_m, 1)) * kRT;
+  // workgroup-uniform: invalid problems, alpha = 0 (no dot product) and tiles past the problem
+  if (N < 1 || N > kMaxModuli || m <= 0 || n <= 0 || r0 >= m || c0 >= n || pr.alpha == 0.0) return;
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const double alpha = pr.alpha, beta = pr.beta;
+  const int mb = (m + 15) >> 4;
+  if (t < 64) {   // word t % 4 of block t / 4 = (bi, bj) = (t / 4 % 4, t / 16)
+    const int bi = (r0 >> 4) + ((t >> 2) & 3), bj = (c0 >> 4) + (t >> 4);
+    const uint64_t v = (bi < mb && bj * 16 < n) ? gp(yds[pi].F)[4 * ((size_t)bj * mb + bi) + (t & 3)] : 0ull;
+    fl[t] = v;
+    int c = __popcll(v);
+#pragma unroll
+    for (int o = 32; o; o >>= 1) c += __shfl_down(c, o);
+    if (t == 0) { cnt[0] = c; cnt[1] = 0; }
+  }
+  lds_sync();
+  const int total = cnt[0];
+  if (total == 0) return;   // workgroup-uniform
+  if (total >= kDenseMin) {
+    dense_dots(pr, r0, c0, fl, buf);
+    return;
+  }
+  const int j = c0 + 16 * w + (lane & 15);
+  for (int bi = 0; bi < 4; ++bi) {   // wave w: the blocks (bi, w)
+    const int i0 = r0 + 16 * bi + 4 * (lane >> 4);
+    unsigned dm = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dm |= (unsigned)((fl[4 * (4 * w + bi) + e] >> lane) & 1u) << e;
+    GLOBAL double* const cp = gpw(pr.C) + (dm ? i0 + (size_t)j * pr.ldc : 0);
+    if (__popcll(__ballot(dm != 0u)) >= kWaveDots) {   // wave-uniform
+      double acc[4];
+      wave_dots(pr, r0 + 16 * bi, c0 + 16 * w, lane, buf + w * kWaveLds, buf + w * kWaveLds + 16 * kKC, acc);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if ((dm >> e) & 1u) cp[e] = from_dot(alpha, beta, acc[e], beta != 0.0 ? cp[e] : 0.0);
+    } else if (dm) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if ((dm >> e) & 1u) {
+          const int x = atomicAdd(&cnt[1], 1);
+          if (x < kListCap) list[x] = (uint32_t)(i0 + e - r0) | ((uint32_t)(j - c0) << 16);
+          else cp[e] = from_dot(alpha, beta, fp64_dot(pr, i0 + e, j), beta != 0.0 ? cp[e] : 0.0);
+        }
+    }
+  }
+  lds_sync();
+  const int L = min(cnt[1], kListCap);
+  if (L > 0) sparse_dots(pr, r0, c0, list, L, buf);   // L is workgroup-uniform
+}
+
 }  // namespace
 
 int recon_launch(const oz2_problem* d, const YDesc* yd, int num, int max_m, int max_n, hipStream_t s, int mode,
-                 bool blocked) {
+                 bool blocked, int* launches, const ReconGrid* grid) {
+  if (launches) *launches = 0;
   if (num <= 0) return 0;
   if (mode != OZ2_REPAIR_OFF && mode != OZ2_REPAIR_COUNT && mode != OZ2_REPAIR_ON) return 1;
   if (num > 65535 || max_m < 0 || max_n < 0) return 1;
@@ -461,20 +736,36 @@ int recon_launch(const oz2_problem* d, const YDesc* yd, int num, int max_m, int 
   if (!c) return 2;
   const size_t mn = (size_t)max_m * (size_t)max_n;
   if (mn == 0) return 0;
-  // tiles of the largest problem; a problem with fewer tiles returns from the surplus workgroups
   const bool blk = blocked && yd;
+  const bool compact = grid && yd && grid->ne == num;
   const int tm = blk ? kBTileM : kTileM, tn = blk ? kBTileN : kTileN;
-  const size_t gx = (size_t)((max_m + tm - 1) / tm) * (size_t)((max_n + tn - 1) / tn);
-  if (gx > 0x7fffffffu) return 1;
-  if (blk)
-    hipLaunchKernelGGL((recon_kernel<true, true>), dim3((unsigned)gx, num), dim3(kThreads), 0, s, d, yd, mode, c->tab,
-                       c->counters);
-  else if (yd)
-    hipLaunchKernelGGL((recon_kernel<true, false>), dim3((unsigned)gx, num), dim3(kThreads), 0, s, d, yd, mode,
-                       c->tab, c->counters);
-  else
-    hipLaunchKernelGGL((recon_kernel<false, false>), dim3((unsigned)gx, num), dim3(kThreads), 0, s, d, nullptr, mode,
-                       c->tab, c->counters);
+  static_assert(kBTileM == kReconTileMB && kBTileN == kReconTileNB && kTileM == kReconTileMC && kTileN == kReconTileNC &&
+                    kRT == kDotTile, "reconstruct tile shapes");
+  // compact grid: the tiles of all problems; else a row per problem as wide as the largest problem
+  // (a problem with fewer tiles returns from the surplus workgroups)
+  const size_t gx = compact ? (size_t)grid->tiles : (size_t)((max_m + tm - 1) / tm) * (size_t)((max_n + tn - 1) / tn);
+  const size_t gd = compact ? (size_t)grid->dtiles : (size_t)((max_m + kRT - 1) / kRT) * (size_t)((max_n + kRT - 1) / kRT);
+  if (gx > 0x7fffffffu || gd > 0x7fffffffu) return 1;
+  const unsigned gy = compact ? 1u : (unsigned)num;
+  const int gne = compact ? num : 0, gper = compact ? grid->per : 0, dper = compact ? grid->dper : 0;
+  int nl = 0;
+  if (gx > 0) {
+    if (blk)
+      hipLaunchKernelGGL((recon_kernel<true, true>), dim3((unsigned)gx, gy), dim3(kThreads), 0, s, d, yd, mode, c->tab,
+                         c->counters, gne, gper);
+    else if (yd)
+      hipLaunchKernelGGL((recon_kernel<true, false>), dim3((unsigned)gx, gy), dim3(kThreads), 0, s, d, yd, mode,
+                         c->tab, c->counters, gne, gper);
+    else
+      hipLaunchKernelGGL((recon_kernel<false, false>), dim3((unsigned)gx, gy), dim3(kThreads), 0, s, d, nullptr, mode,
+                         c->tab, c->counters, 0, 0);
+    ++nl;
+  }
+  if (blk && gd > 0) {
+    hipLaunchKernelGGL(dots_kernel, dim3((unsigned)gd, gy), dim3(kThreads), 0, s, d, yd, gne, dper);
+    ++nl;
+  }
+  if (launches) *launches = nl;
   return hipGetLastError() == hipSuccess ? 0 : 3;
 }
 

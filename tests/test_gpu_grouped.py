@@ -108,7 +108,13 @@ def device_model():
     return dm
 
 
-def check_case(case, path, cfg, st, mode):
+# kernels of one emulated group call besides prep and the INT8 GEMM: the reconstruct, plus the
+# dot-product pass with the blocked digit layout (the default; GGEMM_DIGITS_COLMAJOR=1 turns it off)
+def recon_launches(blocked=True):
+    return 2 if blocked else 1
+
+
+def check_case(case, path, cfg, st, mode, blocked=True):
     """Each problem vs the oracle: bitwise for emulated routes, gamma_n gate for native routes.
     Returns the oracle's counters {uncertified, repaired, safety}."""
     plan_path = G.PATH_EMU_LOOP if path == G.PATH_EMU_LOOP_BATCHED else path
@@ -135,12 +141,13 @@ def check_case(case, path, cfg, st, mode):
     assert st.num_fallback == nfb
     n_emu = sum(1 for e in plan if e.route == 0)
     n_nat = sum(1 for e in plan if e.route not in (0, 1))
+    rl = recon_launches(blocked)
     if path in (G.PATH_EMU_GROUPED, G.PATH_AUTO):
-        want = (3 if n_emu else 0) + (1 if n_nat else 0)
+        want = (2 + rl if n_emu else 0) + (1 if n_nat else 0)
     elif path == G.PATH_EMU_LOOP:
-        want = sum(e.num_moduli + 3 for e in plan if e.route == 0) + (1 if n_nat else 0)
+        want = sum(e.num_moduli + 2 + rl for e in plan if e.route == 0) + (1 if n_nat else 0)
     else:
-        want = 3 * n_emu + (1 if n_nat else 0)
+        want = (2 + rl) * n_emu + (1 if n_nat else 0)
     assert st.kernel_launches == want, (st.kernel_launches, want)
     if nmax:
         assert (st.moduli_min, st.moduli_max) == (nmin, nmax)
@@ -159,7 +166,7 @@ def test_config1_plumbing_fixed_n14():
     cfg = G.Config(14, 1e-15, 1, 0)
     rc, st = run(case, G.PATH_EMU_GROUPED, cfg)
     assert rc == 0
-    assert st.kernel_launches == 3 and st.moduli_min == st.moduli_max == 14 and st.num_fallback == 0
+    assert st.kernel_launches == 2 + recon_launches() and st.moduli_min == st.moduli_max == 14 and st.num_fallback == 0
     check_case(case, G.PATH_EMU_GROUPED, cfg, st, O.REPAIR_COUNT)
 
 
@@ -237,7 +244,7 @@ def run_kernel(case, kernel, cfg=CFG_EMU, **env):
         if env.get("GGEMM_I8_SCHED") == "persistent":
             want = want.replace("_kernel", "_persistent_kernel")
         assert G.lib().ggemm_profile_i8_kernel().decode() == want
-        check_case(case, G.PATH_EMU_GROUPED, cfg, st, O.REPAIR_COUNT)
+        check_case(case, G.PATH_EMU_GROUPED, cfg, st, O.REPAIR_COUNT, blocked=env.get("GGEMM_DIGITS_COLMAJOR") != "1")
         return [case.C(g).copy() for g in range(len(case.hp))]
 
 
@@ -322,7 +329,7 @@ def test_default_layout_long_k_matches_oracle():
         with kernel_handle(case, kernel) as h:
             rc, st = run(case, G.PATH_EMU_GROUPED, cfg, handle=h)
             assert rc == 0 and G.lib().ggemm_profile_i8_kernel().decode() == name
-        assert (st.moduli_min, st.moduli_max, st.kernel_launches) == (15, 16, 3)
+        assert (st.moduli_min, st.moduli_max, st.kernel_launches) == (15, 16, 2 + recon_launches())
         for g, (Co, cnt) in enumerate(want):
             assert same_bits(case.C(g), Co), f"{name}: problem {g} differs"
         assert st.num_uncertified == sum(int(c[1]) for _, c in want)
@@ -384,6 +391,38 @@ def test_hard_numerics_nan_inf_and_repair():
     rc, st = run(case, G.PATH_AUTO, CFG_AUTO)
     assert rc == 0
     check_case(case, G.PATH_AUTO, CFG_AUTO, st, O.REPAIR_ON)
+
+
+@pytest.mark.parametrize("k", [5, 16, 17, 40, 333])
+def test_dense_and_sparse_dot_forms(k):
+    """The reconstruct's FP64 dot-product forms against the oracle's chains, bit for bit, COUNT and
+    ON: tiles whose NaN / Inf rows and columns put more than a quarter of their entries on the safety
+    fallback (dense form, k-chunks of 16 with a partial last chunk for k % 16 != 0 and a single
+    partial chunk for k < 16), tiles with a few such rows (per-block form), and repairs scattered
+    over clean tiles (per-workgroup list); ragged m, n, alpha != 1, beta != 0."""
+    shapes = [(70, 130, k, -1.5, 0.75), (130, 70, k, 2.0, -0.5), (64, 64, k, 1.0, 0.0), (200, 17, k, 0.5, 1.0)]
+    case = Case(shapes, 20261216 + k, phi=3.0)
+    rng = np.random.default_rng(k)
+    h = case.hp[0]          # dense: every fifth row of A and every seventh column of B
+    for r in range(0, h.m, 5):
+        h.A[r + (k // 2) * h.lda] = np.nan
+    for c in range(0, h.n, 7):
+        h.B[(k - 1) + c * h.ldb] = np.inf
+    h = case.hp[1]          # per block: two rows
+    h.A[3 + 0 * h.lda] = -np.inf
+    h.A[100 + (k - 1) * h.lda] = np.nan
+    h = case.hp[3]          # dense by columns only
+    for c in range(0, h.n, 2):
+        h.B[int(rng.integers(0, k)) + c * h.ldb] = np.nan
+    case.alloc()
+    for mode in (G.REPAIR_COUNT, G.REPAIR_ON):
+        say(f"dot forms k={k} mode={mode}")
+        cfg = G.Config(0, 1e-15, 1, mode)
+        with G.Handle(len(shapes), *case.sizes(), min_k=1) as hd:
+            rc, st = run(case, G.PATH_EMU_GROUPED, cfg, handle=hd)
+        assert rc == 0
+        tot = check_case(case, G.PATH_EMU_GROUPED, cfg, st, O.REPAIR_ON if mode == G.REPAIR_ON else O.REPAIR_COUNT)
+        assert tot[3] > 0
 
 
 def test_edge_cases():
@@ -506,7 +545,7 @@ def test_launch_count_independent_of_group_size():
         rc, st = run(case, G.PATH_EMU_GROUPED, CFG_EMU)
         assert rc == 0
         launches.append(st.kernel_launches)
-    assert launches[0] == launches[1] == 3
+    assert launches[0] == launches[1] == 2 + recon_launches()
 
 
 @pytest.mark.parametrize("path", [G.PATH_EMU_GROUPED, G.PATH_AUTO, G.PATH_NATIVE_GROUPED])
