@@ -156,11 +156,20 @@ int i8_launch(const i8_problem* d_probs, const I8Epi* d_epi, const void* d_sched
 // every block of the problem, read by the dot-product pass.
 // t0 / d0: the problem's first tile in the grouped call's compact reconstruct / dot-product grid (the
 // tiles of all problems back to back, so no workgroup of the grid lies outside its problem).
+// nf (blocked layout, or nullptr): kNfWords words per row of A (row i at nf + kNfWords i) and per
+// column of B (column j at nf + kNfWords (m + j)), written by prep for the rows / columns that hold a
+// NaN or an Inf (the others are never written nor read):
+//   word 0: bit 0 a NaN, bit 1 more than kNfCap infinities, bits 8.. the infinities listed (<= kNfCap)
+//   word 1: ilogb of the largest finite nonzero magnitude, kNfNoFinite if there is none
+//   words 2 ..: the infinities' positions k, bit 31 set for -Inf (any order)
+// The dot-product pass evaluates the safety-fallback entries of such rows / columns from them.
+constexpr int kNfWords = 16, kNfCap = kNfWords - 2, kNfNoFinite = -2000;
 struct YDesc {
   const uint8_t* Y;
   size_t y_stride;
   const int32_t* L;
   uint64_t* F;
+  int32_t* nf;
   int t0, d0;
 };
 // Compact grids of a grouped call (ne problems): tiles in all and, when every problem has the same
@@ -185,8 +194,9 @@ int f64_launch(const F64Problem* d_probs, const void* d_sched, int launch, hipSt
 // CRT inverse of modulus l for the problem's N; the abs plane and B are unchanged.
 // fold_q: A residues carry the CRT inverses (production); packed: residue planes in the packed layout
 // max_moduli: the largest num_moduli among the num problems (selects the digit width)
+// yd (or nullptr): descriptors parallel to d whose nf summaries prep writes
 int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t s, int fold_q, int packed,
-                int max_moduli);
+                int max_moduli, const YDesc* yd = nullptr);
 // yd == nullptr: read the int32 planes of oz2_problem::C32 (kernel-level API); else the digits.
 // blocked: the digits and L of every problem are in the blocked layout (production, yd != nullptr);
 // the reconstruct then flags the entries that take FP64 dot products and a second kernel computes
@@ -237,4 +247,6 @@ struct ggemm_handle_s {
   int f64_tile;        // GGEMM_F64_TILE at create: 0 automatic, 64 or 128 forces the native GEMM's tile edge
   int packed_max_kp;   // GGEMM_PACKED_MAX_KP at create: calls whose largest Kp is at most this use packed residues
   int i8_persistent;   // GGEMM_I8_SCHED=persistent at create: the persistent work-stealing INT8 kernels
+  int safety_chains;   // GGEMM_SAFETY_CHAINS=1 at create: safety-fallback entries always run their fma
+                       // chains instead of being decided from prep's non-finite summaries (testing)
 };

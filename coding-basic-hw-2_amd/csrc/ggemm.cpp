@@ -222,16 +222,20 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
   // product workspace (the C32 buffer): CRT digit planes [plane < nmax][problem] of SY bytes
   // each, then the int32 abs-plane products.  Column-major fits because nmax SY + 4 SC <=
   // pmax 4 SC; the blocked layout (whole 16 x 16 blocks) is used when its padded planes fit too.
-  // The blocked layout also keeps the dot-product flags (32 bytes per 16 x 16 block) after the L planes.
-  size_t SY = 0, SYb = 0, SLb = 0, SFb = 0;
+  // The blocked layout also keeps the dot-product flags (32 bytes per 16 x 16 block) after the L planes,
+  // and after them, when they fit and every problem preps its own operands, the non-finite row /
+  // column summaries (kNfWords words per row and column).
+  size_t SY = 0, SYb = 0, SLb = 0, SFb = 0, SNF = 0;
   for (int j = 0; j < c.ne; ++j) {
     const ggemm_problem_t& p = probs[emu_idx[j]];
     SY += align_up((size_t)p.m * p.n, kBufAlign);
     SYb += align_up(blocked_plane_entries(p.m, p.n), kBufAlign);
     SLb += align_up(blocked_plane_entries(p.m, p.n), kBufAlign / 4) * sizeof(int32_t);
     SFb += align_up(blocked_plane_entries(p.m, p.n) / 8, kBufAlign);
+    SNF += align_up((size_t)(p.m + p.n) * kNfWords * sizeof(int32_t), kBufAlign);
   }
   c.blocked = !h->digits_colmajor && (size_t)nmax * SYb + SLb + SFb <= h->C32_bytes;
+  const bool nfsum = c.blocked && !rp && !h->safety_chains && (size_t)nmax * SYb + SLb + SFb + SNF <= h->C32_bytes;
   // Packed residue planes make every 64-byte k-stage of a tile's rows contiguous, which the INT8
   // GEMM's operand stream prefers at moderate k (measured: 1024^3 products 14 % faster together
   // with the blocked digits); at k = 16384 the row-major planes stream better (5 % slower packed).
@@ -242,7 +246,8 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
   uint8_t* ybase = reinterpret_cast<uint8_t*>(h->C32);
   int32_t* lbase = reinterpret_cast<int32_t*>(ybase + (size_t)nmax * SY);
   uint8_t* fbase = reinterpret_cast<uint8_t*>(lbase) + SLb;
-  size_t oa = 0, ob = 0, orow = 0, ocol = 0, q = 0, oy = 0, ol = 0, of = 0;
+  uint8_t* nbase = fbase + SFb;
+  size_t oa = 0, ob = 0, orow = 0, ocol = 0, q = 0, oy = 0, ol = 0, of = 0, onf = 0;
   for (int j = 0; j < c.ne; ++j) {
     const int g = emu_idx[j];
     const ggemm_problem_t& p = probs[g];
@@ -270,6 +275,7 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
     yd.y_stride = SY;
     yd.L = lbase + ol;
     yd.F = c.blocked ? reinterpret_cast<uint64_t*>(fbase + of) : nullptr;
+    yd.nf = nfsum ? reinterpret_cast<int32_t*>(nbase + onf) : nullptr;
     {   // compact reconstruct / dot-product grids
       const int rm = c.blocked ? kReconTileMB : kReconTileMC, rn = c.blocked ? kReconTileNB : kReconTileNC;
       const long long rt = (long long)((p.m + rm - 1) / rm) * ((p.n + rn - 1) / rn);
@@ -305,6 +311,7 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
     oy += align_up(plane, kBufAlign);
     ol += align_up(plane, kBufAlign / 4);
     of += align_up(blocked_plane_entries(p.m, p.n) / 8, kBufAlign);
+    onf += align_up((size_t)(p.m + p.n) * kNfWords * sizeof(int32_t), kBufAlign);
     oa += align_up((size_t)p.m * kp, kBufAlign);
     ob += align_up((size_t)p.n * kp, kBufAlign);
     orow += align_up((size_t)OZ2_ROW_WS_PER_ROW * p.m, 64);
@@ -355,7 +362,8 @@ int enqueue_grouped(const GroupedCall& c, const char* db, hipStream_t s, int rep
   if (c.ne > 0) {
     const bool shared = c.nprep > 0;   // operand reuse: prep once per unique operand
     if (prep_launch(shared ? reinterpret_cast<const oz2_problem*>(db + c.L.off_prep) : doz, shared ? c.nprep : c.ne,
-                    shared ? c.pmax_m : c.max_m, shared ? c.pmax_n : c.max_n, s, 1, c.packed, c.nmax))
+                    shared ? c.pmax_m : c.max_m, shared ? c.pmax_n : c.max_n, s, 1, c.packed, c.nmax,
+                    shared ? nullptr : dyd))
       return GGEMM_ERR_NUMERICS;
     ++*launches;
     prof::mark(prof_set, 1, s);
@@ -526,7 +534,7 @@ int path_emu_loop(ggemm_handle_t h, bool batched, const ggemm_problem_t* probs, 
   const int i8k = h->i8_persistent ? kI8Persistent : kI8General;
   for (int j = 0; j < c.ne && !r; ++j) {
     const int planes = hoz[j].num_moduli + OZ2_EXTRA_PLANES;
-    if (prep_launch(doz + j, 1, hoz[j].m, hoz[j].n, h->stream, 1, c.packed, hoz[j].num_moduli)) {
+    if (prep_launch(doz + j, 1, hoz[j].m, hoz[j].n, h->stream, 1, c.packed, hoz[j].num_moduli, dyd + j)) {
       r = GGEMM_ERR_NUMERICS;
       break;
     }
@@ -738,6 +746,8 @@ extern "C" int ggemm_create_ex(ggemm_handle_t* out, int max_problems, size_t max
   h->i8_persistent = (esc && !std::strcmp(esc, "persistent")) ? 1 : 0;
   const char* epk = std::getenv("GGEMM_PACKED_MAX_KP");
   h->packed_max_kp = epk ? std::max(0, std::atoi(epk)) : kPackedMaxKp;
+  const char* esf = std::getenv("GGEMM_SAFETY_CHAINS");
+  h->safety_chains = (esf && std::atoi(esf) == 1) ? 1 : 0;
   if (hipStreamSynchronize(stream) != hipSuccess) FAIL(GGEMM_ERR_CUDA);
 #undef HIPA
 #undef FAIL

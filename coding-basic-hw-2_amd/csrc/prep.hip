@@ -221,13 +221,49 @@ struct PrepShared {
   int shift[kARows], sig[kARows];
   double rowmax[kARows];
   double tile[kATile][kARows];      // A values of the current k-tile, k-major
+  // non-finite summaries of the block's rows (A) or columns (B, slot = the column's 32-lane group):
+  // infinities listed so far, NaN seen, largest finite magnitude (bits of a non-negative double)
+  int nfcnt[kARows], nfnan[kARows];
+  unsigned long long nfmx[kARows];
 };
+
+// One row's / column's values a[e] at k = kb + ks e (zeros past K) into its summary: infinities
+// listed at nfw + 2 .. (slots from an LDS counter, any order), NaN and the largest finite magnitude
+// into LDS.  The summary state stays in LDS, so none of it is live across the residue loops.
+__device__ __forceinline__ void nf_scan(const double (&a)[4], int kb, int ks, GLOBAL int32_t* nfw, int* ncnt, int* nnan,
+                                        unsigned long long* nmx) {
+  double mt = 0.0;
+  bool nn = false;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if (isnan(a[e])) {
+      nn = true;
+    } else if (isinf(a[e])) {
+      const int x = atomicAdd(ncnt, 1);
+      if (x < kNfCap) nfw[2 + x] = (kb + ks * e) | (a[e] < 0.0 ? (int)0x80000000u : 0);
+    } else {
+      mt = fmax(mt, fabs(a[e]));
+    }
+  }
+  if (nn) *nnan = 1;
+  if (mt > 0.0) atomicMax(nmx, (unsigned long long)__double_as_longlong(mt));
+}
+// The summary's words 0 and 1 from the LDS state.
+__device__ __forceinline__ void nf_header(GLOBAL int32_t* nfw, int ni, int nan, unsigned long long mx) {
+  nfw[0] = (nan ? 1 : 0) | (ni > kNfCap ? 2 : 0) | (min(ni, kNfCap) << 8);
+  nfw[1] = mx ? ilogb(__longlong_as_double((long long)mx)) : kNfNoFinite;
+}
 
 // ------------------------------------------------------------------------------- A rows
 template <bool kWide>
 __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ tab, int blk, int split,
-                          int nsplit, PrepShared& sm, unsigned long long* cnt, int widx, bool packed) {
+                          int nsplit, PrepShared& sm, unsigned long long* cnt, int widx, bool packed, int32_t* nfo) {
   const int tid = threadIdx.x;
+  if (tid < kARows) {   // ordered before their atomics by the barriers of pass 1
+    sm.nfcnt[tid] = 0;
+    sm.nfnan[tid] = 0;
+    sm.nfmx[tid] = 0ull;
+  }
   const int N = pr.num_moduli, K = pr.k, Kp = pr.kp, m = pr.m;
   const int row0 = blk * kARows;
   const int r = tid & 31, c = tid >> 5;          // chain role: row r, chain c
@@ -301,6 +337,9 @@ __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ t
   const bool nf_r = sh_r == OZ2_SHIFT_NONFINITE;
   const bool rvalid = row0 + rr < m;
   double da2 = 0.0, na2 = 0.0;
+  // split 0, rows holding a NaN / Inf, when the call asks for summaries: whether a NaN occurs, the
+  // largest finite magnitude and the infinities' positions, from the values this pass loads anyway
+  const bool nfr = nfo && nf_c && valid && split == 0;
   const int ntile = (Kp + kATile - 1) / kATile;
   const int per = (ntile + nsplit - 1) / nsplit;
   const int w0 = min(ntile, split * per), w1 = min(ntile, w0 + per);   // tiles written here
@@ -312,6 +351,14 @@ __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ t
     for (int jj = 0; jj < kATile / kChains; ++jj) {
       const int k = k0 + c + kChains * jj;
       av[jj] = (valid && k < K) ? A[i + (size_t)k * lda] : 0.0;
+    }
+    if (nfr) {
+      GLOBAL int32_t* const nfw = (GLOBAL int32_t*)nfo + (size_t)kNfWords * i;
+#pragma unroll
+      for (int g = 0; g < kATile / kChains / 4; ++g) {
+        const double a[4] = {av[4 * g], av[4 * g + 1], av[4 * g + 2], av[4 * g + 3]};
+        nf_scan(a, k0 + c + kChains * 4 * g, kChains, nfw, &sm.nfcnt[r], &sm.nfnan[r], &sm.nfmx[r]);
+      }
     }
     if (!nf_c && split == 0) {
       double xs[kATile / kChains];
@@ -360,6 +407,7 @@ __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ t
   if (c == 0 && valid) {
     double D = 0.0, Nn = 0.0;
     for (int q = 0; q < kChains; ++q) { D += sm.red0[q][r]; Nn += sm.red1[q][r]; }
+    if (nfr) nf_header((GLOBAL int32_t*)nfo + (size_t)kNfWords * i, sm.nfcnt[r], sm.nfnan[r], sm.nfmx[r]);
     ((GLOBAL int32_t*)pr.row_shift)[2 * m + i] = norm_ub_bits(D);
     ((GLOBAL int32_t*)pr.row_shift)[3 * m + i] = norm_ub_bits(Nn);
   }
@@ -370,11 +418,19 @@ constexpr int kBReg = 32;   // column values per lane held in registers (K <= 32
 
 template <bool kWide>
 __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ tab, int blk, int split,
-                          int nsplit, PrepShared& sm, unsigned long long* cnt, bool packed) {
+                          int nsplit, PrepShared& sm, unsigned long long* cnt, bool packed, int32_t* nfo) {
   const int lane = threadIdx.x & 31, w = threadIdx.x >> 5;
   const int j = blk * kBCols + w;
   const int n = pr.n, N = pr.num_moduli, K = pr.k, Kp = pr.kp;
   if (j >= n) return;   // no barriers below; the 32-lane group is column-uniform
+  if (nfo && lane == 0) {   // the column's summary state (used by this 32-lane group only)
+    sm.nfcnt[w] = 0;
+    sm.nfnan[w] = 0;
+    sm.nfmx[w] = 0ull;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   const GLOBAL double* __restrict__ b = (const GLOBAL double*)pr.B + (size_t)j * pr.ldb;
   const double T = tab->T[N];
 
@@ -441,6 +497,13 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
   }
   const bool nf = sh == OZ2_SHIFT_NONFINITE;
 
+  // split 0, columns holding a NaN / Inf, when the call asks for summaries (column-uniform)
+  const bool nfc = nfo && nf && split == 0;
+  auto nfw = [&]() { return (GLOBAL int32_t*)nfo + (size_t)kNfWords * ((size_t)pr.m + j); };
+  auto nfscan = [&](const double (&a)[4], int kb, int ks) {
+    nf_scan(a, kb, ks, nfw(), &sm.nfcnt[w], &sm.nfnan[w], &sm.nfmx[w]);
+  };
+
   double da2 = 0.0, na2 = 0.0;
   GLOBAL int8_t* const B8 = (GLOBAL int8_t*)pr.B8;
   const int nchunk = (Kp + 127) / 128;
@@ -482,6 +545,13 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
     // lane l holds k = 128 ch + 32 jj + l (jj < 4) of chunk ch in v[4 ch + jj]: through this column's
     // LDS exchange row to k = 128 ch + 4 l + e; unrolled so that the register indices are static
     double* const xb = reinterpret_cast<double*>(&sm.tile[0][0]) + 128 * w;
+    if (nfc) {   // the lane's own values, k = l + 32 t
+#pragma unroll
+      for (int g = 0; g < kBReg / 4; ++g) {
+        const double a[4] = {v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]};
+        nfscan(a, lane + 128 * g, 32);
+      }
+    }
 #pragma unroll
     for (int ch = 0; ch < kBReg / 4; ++ch) {
       if (ch < ch0 || ch >= ch1) continue;   // column-uniform
@@ -497,6 +567,18 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       chunk(ch, a);
+    }
+  } else if (nfc) {   // a summary column: the values only for the summary, zero residues
+    for (int ch = ch0; ch < ch1; ++ch) {
+      const int k0 = 128 * ch + 4 * lane;
+      double a[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) a[e] = (k0 + e < K) ? b[k0 + e] : 0.0;
+      nfscan(a, k0, 1);
+      if (k0 < Kp && ch >= c0 && ch < c1)
+        for (int l = 0; l <= N; ++l)
+          *(GLOBAL uint32_t*)(B8 + (packed ? packed_offset(j, k0, n, Kp) : (size_t)j * Kp + k0) +
+                              (size_t)l * pr.b8_mod_stride) = 0u;
     }
   } else {
     for (int ch = ch0; ch < ch1; ++ch) {
@@ -517,6 +599,12 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
     ((GLOBAL int32_t*)pr.col_shift)[2 * n + j] = norm_ub_bits(da2);
     ((GLOBAL int32_t*)pr.col_shift)[3 * n + j] = norm_ub_bits(na2);
   }
+  if (nfc) {   // every lane's LDS updates precede lane 0's reads
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane == 0) nf_header(nfw(), sm.nfcnt[w], sm.nfnan[w], sm.nfmx[w]);
+  }
 }
 
 // kWide: three-word digits (any N); the two-word kernel is launched only for calls whose every
@@ -525,9 +613,10 @@ template <bool kWide>
 __global__ void __launch_bounds__(kThreads, 4) prep_kernel(const oz2_problem* __restrict__ probs, int a_blocks,
                                                         const CrtTables* __restrict__ tab,
                                                         unsigned long long* __restrict__ cnt, int fold_q,
-                                                        int packed) {
+                                                        int packed, const YDesc* __restrict__ yds) {
   __shared__ PrepShared sm;
   const oz2_problem& pr = probs[blockIdx.y];
+  int32_t* const nfo = yds ? yds[blockIdx.y].nf : nullptr;
   const int N = pr.num_moduli;
   if (N < 1 || N > kMaxModuli || pr.alpha == 0.0) return;   // alpha == 0: A, B never referenced
   // folded A residues use the weights q 2^(8 i) mod p, so that sum b_i [q 2^(8 i)] = q x (mod p)
@@ -535,9 +624,9 @@ __global__ void __launch_bounds__(kThreads, 4) prep_kernel(const oz2_problem* __
   const int blk = (int)blockIdx.x;
   if (blk < a_blocks) {
     if (blk * kARows >= pr.m) return;
-    prep_rows<kWide>(pr, tab, blk, blockIdx.z, gridDim.z, sm, cnt, fold ? N : 0, packed != 0);
+    prep_rows<kWide>(pr, tab, blk, blockIdx.z, gridDim.z, sm, cnt, fold ? N : 0, packed != 0, nfo);
   } else {
-    prep_cols<kWide>(pr, tab, blk - a_blocks, blockIdx.z, gridDim.z, sm, cnt, packed != 0);
+    prep_cols<kWide>(pr, tab, blk - a_blocks, blockIdx.z, gridDim.z, sm, cnt, packed != 0, nfo);
   }
 }
 
@@ -546,7 +635,7 @@ int g_force_split = 0;
 }  // namespace
 
 int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t s, int fold_q, int packed,
-                int max_moduli) {
+                int max_moduli, const YDesc* yd) {
   if (num <= 0) return 0;
   if (num > 65535 || max_m < 0 || max_n < 0 || max_moduli < 1 || max_moduli > kMaxModuli) return 1;
   DevCtx* c = dev_ctx();
@@ -562,10 +651,10 @@ int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t
   if (!ht) return 2;
   if (ht->T[max_moduli] < 0x1.8p62)
     hipLaunchKernelGGL(prep_kernel<false>, dim3(a_blocks + b_blocks, num, S), dim3(kThreads), 0, s, d, a_blocks,
-                       c->tab, c->counters, fold_q, packed);
+                       c->tab, c->counters, fold_q, packed, yd);
   else
     hipLaunchKernelGGL(prep_kernel<true>, dim3(a_blocks + b_blocks, num, S), dim3(kThreads), 0, s, d, a_blocks,
-                       c->tab, c->counters, fold_q, packed);
+                       c->tab, c->counters, fold_q, packed, yd);
   return hipGetLastError() == hipSuccess ? 0 : 3;
 }
 

@@ -495,6 +495,8 @@ __global__ void __launch_bounds__(kThreads) recon_kernel(const oz2_problem* __re
 //     all 256 threads stage their A rows and B columns through LDS in k-chunks of 64 to 1024 (all
 //     of a chunk's loads in flight together, the next chunk's while the chains run), one lane per
 //     chain -- instead of one lane loading its A row, lda apart, and its B column itself.
+// Before that, the safety-fallback entries are evaluated from prep's non-finite summaries when the
+// call has them (nf_dot below); only those it cannot decide, and the repairs, take the chains.
 constexpr int kRT = 64;            // tile rows and columns
 constexpr int kDenseMin = 1024;    // flagged entries of a tile from which it takes the dense form
 constexpr int kDK = 8;             // dense k-chunk
@@ -505,6 +507,61 @@ constexpr int kUnion = 4 * kWaveLds;                  // wave_dots x 4 waves; >=
 static_assert(4 * kDK * kRT <= kUnion && 2 * 1024 <= kUnion, "dot-pass LDS union");
 
 __device__ __forceinline__ void lds_sync() { __syncthreads(); }
+
+// The fp64 dot product of a safety-fallback entry (row i of A or column j of B holds a NaN or an
+// Inf) without its chain.  The chain s = fma(a_k, b_k, s) from s = 0 ends non-finite: a product
+// with an infinite factor is +-Inf, or NaN when the other factor is 0 or NaN; an infinite s stays
+// so under finite addends and turns NaN under the opposite infinity; NaN stays NaN.  Its value is
+// therefore NaN if a NaN factor occurs, if an infinity meets a zero or if infinite products of both
+// signs occur, and otherwise the one signed infinity -- provided no finite partial sum overflows
+// before the first infinite product.  Those sums stay below k 2^(eA + 1) 2^(eB + 1) (1 + u)^k <
+// 2^(eA + eB + 3 + ceil(log2 k)) (eA, eB: ilogb of the largest finite magnitudes of the row and
+// the column), so eA + eB + 3 + ceil(log2 k) <= 1023 rules overflow out.  Returns false (the entry
+// takes its chain) outside that bound or when the row or column has more infinities than its
+// summary lists.  The result equals the chain's bit for bit except for a NaN's payload.
+// hr / eA: the row's summary words 0 and 1 (rnf) or 0 and its exponent from sigma; likewise hc / eB.
+__device__ __forceinline__ bool nf_dot(const oz2_problem& pr, const GLOBAL int32_t* R, const GLOBAL int32_t* Cl,
+                                       int i, int j, int hr, int eA, int hc, int eB, double& d) {
+  if ((hr | hc) & 1) {
+    d = __builtin_nan("");
+    return true;
+  }
+  const int K = pr.k;
+  const int lk = K > 1 ? 32 - __clz(K - 1) : 0;
+  if (((hr | hc) & 2) || eA + eB + 3 + lk > 1023) return false;
+  bool nan = false, pos = false, neg = false;
+  const int nr = (hr >> 8) & 0xff, nc = (hc >> 8) & 0xff;
+  const GLOBAL double* b = gp(pr.B) + (size_t)j * pr.ldb;
+  for (int s = 0; s < nr; ++s) {   // row infinities: a_k = +-Inf against b_k
+    const int w = R[2 + s];
+    const double x = b[w & 0x7fffffff];
+    if (x == 0.0 || isnan(x)) nan = true;
+    else if ((w < 0) != (x < 0.0)) neg = true;
+    else pos = true;
+  }
+  const GLOBAL double* a = gp(pr.A) + i;
+  for (int s = 0; s < nc; ++s) {   // column infinities: b_k = +-Inf against a_k
+    const int w = Cl[2 + s];
+    const double x = a[(size_t)(w & 0x7fffffff) * pr.lda];
+    if (x == 0.0 || isnan(x)) nan = true;
+    else if ((w < 0) != (x < 0.0)) neg = true;
+    else pos = true;
+  }
+  if (!(nan || pos || neg)) return false;   // no infinity listed (not a safety entry)
+  d = (nan || (pos && neg)) ? __builtin_nan("") : (pos ? __builtin_inf() : -__builtin_inf());
+  return true;
+}
+
+// Flagged entries of the tile counted into *c (threads 0 .. 63 read one flag word each).
+__device__ __forceinline__ void count_flags(const uint64_t* fl, int* c) {
+  const int t = threadIdx.x;
+  if (t < 64) {
+    int v = __popcll(fl[t]);
+#pragma unroll
+    for (int o = 32; o; o >>= 1) v += __shfl_down(v, o);
+    if (t == 0) *c = v;
+  }
+}
 
 // flag of tile entry (il, jl): block b = 4 (jl / 16) + il / 16, word il % 4, bit = MFMA lane
 // 16 ((il % 16) / 4) + jl % 16
@@ -682,16 +739,61 @@ __global__ void __launch_bounds__(kThreads) dots_kernel(const oz2_problem* __res
   const int mb = (m + 15) >> 4;
   if (t < 64) {   // word t % 4 of block t / 4 = (bi, bj) = (t / 4 % 4, t / 16)
     const int bi = (r0 >> 4) + ((t >> 2) & 3), bj = (c0 >> 4) + (t >> 4);
-    const uint64_t v = (bi < mb && bj * 16 < n) ? gp(yds[pi].F)[4 * ((size_t)bj * mb + bi) + (t & 3)] : 0ull;
-    fl[t] = v;
-    int c = __popcll(v);
-#pragma unroll
-    for (int o = 32; o; o >>= 1) c += __shfl_down(c, o);
-    if (t == 0) { cnt[0] = c; cnt[1] = 0; }
+    fl[t] = (bi < mb && bj * 16 < n) ? gp(yds[pi].F)[4 * ((size_t)bj * mb + bi) + (t & 3)] : 0ull;
+    if (t == 0) cnt[1] = 0;
   }
+  count_flags(fl, &cnt[0]);
   lds_sync();
-  const int total = cnt[0];
+  int total = cnt[0];
   if (total == 0) return;   // workgroup-uniform
+  const GLOBAL int32_t* const nf = gp(yds[pi].nf);
+  if (nf) {
+    // safety-fallback entries from the summaries: thread t takes row il = t % 64 of the tile in
+    // columns jl = 16 (t / 64) .. + 15 (the column's summary is wave-uniform, C stores contiguous);
+    // decided entries are stored and their flags cleared
+    const int il = t & 63, i = r0 + il;
+    if (i < m) {
+      const GLOBAL int32_t* rs = gp(pr.row_shift);
+      const GLOBAL int32_t* cs = gp(pr.col_shift);
+      const int rsh = rs[i], sg = rs[m + i];
+      const bool rnf = rsh == OZ2_SHIFT_NONFINITE;
+      const GLOBAL int32_t* R = nf + (size_t)kNfWords * i;
+      int hr = 0, eA = sg == OZ2_SHIFT_ZERO ? kNfNoFinite : 6 - sg;
+      if (rnf) {
+        hr = R[0];
+        eA = R[1];
+      }
+      for (int q = 0; q < 16; ++q) {
+        const int jl = 16 * (t >> 6) + q, j = c0 + jl;
+        const int wi = 4 * (4 * (jl >> 4) + (il >> 4)) + (il & 3);
+        const uint64_t bit = 1ull << (16 * ((il & 15) >> 2) + (jl & 15));
+        if (j >= n || !(fl[wi] & bit)) continue;
+        const int csh = cs[j];
+        const bool cnf = csh == OZ2_SHIFT_NONFINITE;
+        if (!rnf && !cnf) continue;   // a repair
+        const GLOBAL int32_t* Cl = nf + (size_t)kNfWords * ((size_t)m + j);
+        int hc = 0, eB;
+        if (cnf) {
+          hc = Cl[0];
+          eB = Cl[1];
+        } else {
+          const int tau = cs[n + j];
+          eB = tau == OZ2_SHIFT_ZERO ? kNfNoFinite : 6 - tau;
+        }
+        double d;
+        if (nf_dot(pr, R, Cl, i, j, hr, eA, hc, eB, d)) {
+          GLOBAL double* cp = gpw(pr.C) + i + (size_t)j * pr.ldc;
+          *cp = from_dot(alpha, beta, d, beta != 0.0 ? *cp : 0.0);
+          atomicAnd(reinterpret_cast<unsigned long long*>(&fl[wi]), ~(unsigned long long)bit);
+        }
+      }
+    }
+    lds_sync();
+    count_flags(fl, &cnt[0]);
+    lds_sync();
+    total = cnt[0];
+    if (total == 0) return;   // workgroup-uniform
+  }
   if (total >= kDenseMin) {
     dense_dots(pr, r0, c0, fl, buf);
     return;

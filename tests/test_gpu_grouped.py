@@ -393,13 +393,27 @@ def test_hard_numerics_nan_inf_and_repair():
     check_case(case, G.PATH_AUTO, CFG_AUTO, st, O.REPAIR_ON)
 
 
+def env_handle(case, min_k=None, **env):
+    """A handle created with environment variables set (read at creation)."""
+    saved = dict(os.environ)
+    os.environ.update(env)
+    try:
+        return G.Handle(max(len(case.hp), 1), *case.sizes(), min_k=min_k)
+    finally:
+        os.environ.clear()
+        os.environ.update(saved)
+
+
+@pytest.mark.parametrize("chains", [True, False])
 @pytest.mark.parametrize("k", [5, 16, 17, 40, 333])
-def test_dense_and_sparse_dot_forms(k):
+def test_dense_and_sparse_dot_forms(k, chains):
     """The reconstruct's FP64 dot-product forms against the oracle's chains, bit for bit, COUNT and
     ON: tiles whose NaN / Inf rows and columns put more than a quarter of their entries on the safety
     fallback (dense form, k-chunks of 16 with a partial last chunk for k % 16 != 0 and a single
     partial chunk for k < 16), tiles with a few such rows (per-block form), and repairs scattered
-    over clean tiles (per-workgroup list); ragged m, n, alpha != 1, beta != 0."""
+    over clean tiles (per-workgroup list); ragged m, n, alpha != 1, beta != 0.  chains: the safety
+    entries run their fma chains (GGEMM_SAFETY_CHAINS=1), which is what puts tiles on the dense
+    and per-block forms; else they are decided from prep's non-finite summaries."""
     shapes = [(70, 130, k, -1.5, 0.75), (130, 70, k, 2.0, -0.5), (64, 64, k, 1.0, 0.0), (200, 17, k, 0.5, 1.0)]
     case = Case(shapes, 20261216 + k, phi=3.0)
     rng = np.random.default_rng(k)
@@ -416,13 +430,100 @@ def test_dense_and_sparse_dot_forms(k):
         h.B[int(rng.integers(0, k)) + c * h.ldb] = np.nan
     case.alloc()
     for mode in (G.REPAIR_COUNT, G.REPAIR_ON):
-        say(f"dot forms k={k} mode={mode}")
+        say(f"dot forms k={k} mode={mode} chains={chains}")
         cfg = G.Config(0, 1e-15, 1, mode)
-        with G.Handle(len(shapes), *case.sizes(), min_k=1) as hd:
+        with env_handle(case, min_k=1, GGEMM_SAFETY_CHAINS="1" if chains else "0") as hd:
             rc, st = run(case, G.PATH_EMU_GROUPED, cfg, handle=hd)
         assert rc == 0
         tot = check_case(case, G.PATH_EMU_GROUPED, cfg, st, O.REPAIR_ON if mode == G.REPAIR_ON else O.REPAIR_COUNT)
         assert tot[3] > 0
+
+
+def _inf_patterns(seed):
+    """Problems whose NaN / Inf rows and columns cover each case of the summary evaluation, with
+    the full fma chain as the expected value (oracle)."""
+    rng = np.random.default_rng(seed)
+    shapes = [(40, 36, 50, 1.0, 0.0),        # single-read B columns (k <= 1024), ragged tiles
+              (8, 8, 64, 1.0, 0.0),          # overflow bound
+              (70, 66, 90, -1.5, 0.5),       # beta != 0, C0 with NaN / Inf
+              (20, 24, 1500, 2.0, 0.0)]      # B columns read in chunks (k > 1024)
+    case = Case(shapes, seed, phi=1.0)
+    inf, nan = np.inf, np.nan
+    h = case.hp[0]
+    A = lambda i, k: i + k * h.lda
+    B = lambda k, j: k + j * h.ldb
+    h.A[A(0, 3)] = inf                       # +Inf against b = 0 (NaN) and b < 0 (-Inf)
+    h.B[B(3, 0)] = 0.0
+    h.B[B(3, 1)] = -2.0
+    h.A[A(1, 5)] = inf                       # +Inf and -Inf: NaN where the products' signs differ
+    h.A[A(1, 9)] = -inf
+    h.A[A(2, 7)] = nan                       # NaN row
+    for k in range(10, 30):                  # more infinities than the summary lists: chains
+        h.A[A(3, k)] = inf
+    h.B[B(np.arange(10, 30), 2)] = np.abs(h.B[B(np.arange(10, 30), 2)]) + 0.5   # +Inf through the chain
+    h.A[A(4, np.arange(h.k))] = 0.0          # no finite nonzero entry besides the infinity
+    h.A[A(4, 0)] = -inf
+    h.B[B(11, 3)] = inf                      # column infinity against a = 0 (NaN) and a = -Inf
+    h.A[A(5, 11)] = 0.0
+    h.A[A(6, 11)] = -inf
+    h.B[B(20, 4)] = nan                      # NaN column
+    h.A[A(7, 13)] = inf                      # row and column infinity at the same k
+    h.B[B(13, 5)] = -inf
+    h.B[B(33, 6)] = -inf                     # column with two infinities of either sign
+    h.B[B(40, 6)] = inf
+    h = case.hp[1]
+    A = lambda i, k: i + k * h.lda
+    B = lambda k, j: k + j * h.ldb
+    h.A[A(0, np.arange(63))] = 1e300         # finite sum overflows to +Inf before the -Inf: NaN
+    h.A[A(0, 63)] = -inf
+    h.B[B(np.arange(64), 0)] = 1e10
+    h.A[A(1, 0)] = 1e300                     # first product overflows
+    h.A[A(1, 63)] = -inf
+    h.B[B(0, 1)] = 1e300
+    h.B[B(63, 1)] = 1.0
+    h.A[A(2, np.arange(63))] = 1e150         # inside the bound: -Inf
+    h.A[A(2, 63)] = -inf
+    h.B[B(np.arange(64), 2)] = 1e150
+    h = case.hp[2]
+    for _ in range(40):
+        arr, ld, rows, cols = (h.A, h.lda, h.m, h.k) if rng.random() < 0.5 else (h.B, h.ldb, h.k, h.n)
+        arr[int(rng.integers(0, rows)) + int(rng.integers(0, cols)) * ld] = rng.choice([inf, -inf, inf, -inf, nan])
+    h.C0[int(rng.integers(0, h.m)) + np.arange(h.n) * h.ldc] = rng.choice([nan, inf, -inf, 1.0], h.n)
+    h = case.hp[3]
+    for c in range(0, h.n, 3):               # infinities past the first 1024 k
+        h.B[int(rng.integers(1024, h.k)) + c * h.ldb] = rng.choice([inf, -inf])
+    for r in range(0, h.m, 4):
+        h.A[r + int(rng.integers(0, h.k)) * h.lda] = rng.choice([inf, -inf])
+    case.alloc()
+    return case
+
+
+@pytest.mark.parametrize("N", [0, 18])
+def test_safety_entries_from_summaries(N):
+    """Safety-fallback entries decided from prep's non-finite summaries equal the oracle's fma
+    chains bit for bit (NaN payloads aside) in every repair mode -- zero and NaN factors, infinite
+    products of both signs, rows and columns with infinities at the same k, more infinities than a
+    summary lists, finite sums that overflow before the infinity and ones inside the bound, beta
+    C0 non-finite -- and equal a handle that runs every chain.  N = 18: three-word digits."""
+    case = _inf_patterns(20261202 + N)
+    outs = {}
+    for chains in ("0", "1"):
+        for mode, omode in ((G.REPAIR_OFF, O.REPAIR_OFF), (G.REPAIR_COUNT, O.REPAIR_COUNT),
+                            (G.REPAIR_ON, O.REPAIR_ON)):
+            say(f"summaries N={N} chains={chains} mode={mode}")
+            cfg = G.Config(N, 1e-15, 0, mode)
+            with env_handle(case, min_k=1, GGEMM_SAFETY_CHAINS=chains) as hd:
+                rc, st = run(case, G.PATH_EMU_GROUPED, cfg, handle=hd)
+            assert rc == 0
+            tot = check_case(case, G.PATH_EMU_GROUPED, cfg, st, omode)
+            assert tot[3] > 0
+            outs[(chains, mode)] = [case.C(g).copy() for g in range(len(case.hp))]
+    for mode in (G.REPAIR_OFF, G.REPAIR_COUNT, G.REPAIR_ON):
+        for a, b in zip(outs[("0", mode)], outs[("1", mode)]):
+            assert same_bits(a, b)
+    h = case.hp[1]   # the overflow cases are NaN, the bounded one -Inf
+    C1 = outs[("0", G.REPAIR_ON)][1]
+    assert np.isnan(C1[0]) and np.isnan(C1[1 + h.ldc]) and C1[2 + 2 * h.ldc] == -np.inf
 
 
 def test_edge_cases():

@@ -13,6 +13,7 @@ TOOL = Path(__file__).resolve().parents[1] / "coding-basic-hw-2_amd" / "analysis
 PREP = "ggemm::(anonymous namespace)::prep_kernel(oz2_problem const*, int, ggemm::CrtTables const*, unsigned long long*, int)"
 I8 = "ggemm::(anonymous namespace)::i8_large_kernel(i8_problem const*, ggemm::I8Epi const*, int const*)"
 RECON = "void ggemm::(anonymous namespace)::recon_kernel<true>(oz2_problem const*, ggemm::YDesc const*, int)"
+DOTS = "ggemm::(anonymous namespace)::dots_kernel(oz2_problem const*, ggemm::YDesc const*, int, int)"
 F64 = "ggemm::(anonymous namespace)::f64_grouped_kernel(ggemm::F64Problem const*, int const*)"
 TORCH = "void at::native::vectorized_elementwise_kernel<4, at::native::FillFunctor<double> >(int)"
 COPY = "__amd_rocclr_copyBuffer"
@@ -69,8 +70,8 @@ def test_calls_busy_gap_and_stages(tmp_path):
 def test_kernel_names_and_stages():
     rr = _tool()
     assert [rr.short_name(n) for n in (PREP, I8, RECON)] == ["prep_kernel", "i8_large_kernel", "recon_kernel<true>"]
-    assert [rr.stage_of(n) for n in (PREP, I8, RECON, F64, COPY, TORCH)] == \
-        ["prep", "i8_gemm", "reconstruct", "native", "memops", None]
+    assert [rr.stage_of(n) for n in (PREP, I8, RECON, DOTS, F64, COPY, TORCH)] == \
+        ["prep", "i8_gemm", "reconstruct", "reconstruct", "native", "memops", None]
 
 
 def test_roofline_and_traffic(tmp_path):
@@ -126,3 +127,21 @@ def test_traffic_json_record(tmp_path):
     assert rec["fetch_kib"] == pytest.approx(200.0) and rec["write_kib"] == pytest.approx(64.0)
     assert rec["fetch_factor"] == pytest.approx(0.5) and rec["write_factor"] == pytest.approx(1.0)
     assert rec["traffic_bytes"] == round((400 + 64) * 1024)
+
+
+def test_dot_pass_counts_in_reconstruct_without_roofline(tmp_path):
+    """The flagged entries' FP64 dot products (dots_kernel) run after recon_kernel: their time is
+    reconstruct time, but the stage's algorithmic bytes are credited to recon_kernel alone."""
+    rr = _tool()
+    tr = tmp_path / "t.csv"
+    _trace(tr, [(PREP, 0, 100_000), (I8, 100_000, 300_000), (RECON, 300_000, 340_000), (DOTS, 340_000, 400_000)])
+    calls = [rr.call_metrics(c) for c in rr.split_calls(rr.read_trace(tr))]
+    assert [c["kernels"] for c in calls] == [4]
+    assert calls[0]["reconstruct_us"] == pytest.approx(100.0)
+    args = rr.argparse.Namespace(trace=str(tr), workload="2,64,32,100,3", fetch=None, write=None, copy_fetch=None,
+                                 copy_write=None, copy_bytes=float(1 << 30), out=str(tmp_path / "r.md"), csv=None)
+    _, rows = rr.report(args)
+    by = {r["kernel"]: r for r in rows}
+    recon = 2 * ((3 + 4.0) * 64 * 32 + 8.0 * 64 * 32 + 16.0 * (64 + 32))
+    assert by["recon_kernel<true>"]["achieved"] == pytest.approx(recon / 40e-6 / 1e12)
+    assert by["dots_kernel"]["stage"] == "reconstruct" and by["dots_kernel"]["achieved"] is None
