@@ -31,6 +31,7 @@ struct GroupedCall {
   bool packed = false;            // residue planes in the packed layout
   int f64_tiles = 0;              // native GEMM launch word (tile count, kF64Tile128 for 128 x 128 tiles)
   ReconGrid rgrid{};              // compact reconstruct / dot-product grids
+  int dot_form = 0;               // the handle's dot-product form override (kDotForm*)
   size_t h2d_bytes = 0;           // bytes of the blob to copy
 };
 

@@ -203,8 +203,13 @@ int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t
 // them.  *launches (if given) receives the number of kernels launched.
 // grid (production calls): the compact grids of the yd[].t0 / d0 offsets; nullptr: one grid row per
 // problem, as wide as the largest problem's tile count (kernel-level API, per-problem launches).
+// dot_form: the dot-product pass's choice of forms -- kDotFormAuto, or for tests kDotFormDense (every
+// tile with flagged entries computes all its chains), kDotFormBlocks (per-block and listed entries
+// only), kDotFormList (listed entries only)
+enum { kDotFormAuto = 0, kDotFormDense = 1, kDotFormBlocks = 2, kDotFormList = 3 };
 int recon_launch(const oz2_problem* d, const YDesc* yd, int num, int max_m, int max_n, hipStream_t s, int mode,
-                 bool blocked = false, int* launches = nullptr, const ReconGrid* grid = nullptr);
+                 bool blocked = false, int* launches = nullptr, const ReconGrid* grid = nullptr,
+                 int dot_form = kDotFormAuto);
 
 }  // namespace ggemm
 
@@ -249,4 +254,5 @@ struct ggemm_handle_s {
   int i8_persistent;   // GGEMM_I8_SCHED=persistent at create: the persistent work-stealing INT8 kernels
   int safety_chains;   // GGEMM_SAFETY_CHAINS=1 at create: safety-fallback entries always run their fma
                        // chains instead of being decided from prep's non-finite summaries (testing)
+  int dot_form;        // GGEMM_DOT_FORM at create: kDotForm* (testing)
 };

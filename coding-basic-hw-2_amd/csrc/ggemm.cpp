@@ -242,6 +242,7 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
   int max_kp = 0;
   for (int j = 0; j < c.ne; ++j) max_kp = std::max(max_kp, kp_of(probs[emu_idx[j]].k));
   c.packed = !h->digits_colmajor && max_kp <= h->packed_max_kp;
+  c.dot_form = h->dot_form;
   if (c.blocked) SY = SYb;
   uint8_t* ybase = reinterpret_cast<uint8_t*>(h->C32);
   int32_t* lbase = reinterpret_cast<int32_t*>(ybase + (size_t)nmax * SY);
@@ -374,7 +375,8 @@ int enqueue_grouped(const GroupedCall& c, const char* db, hipStream_t s, int rep
     prof::last_i8 = c.i8_kernel;
     prof::mark(prof_set, 2, s);
     int nr = 0;
-    if (recon_launch(doz, dyd, c.ne, c.max_m, c.max_n, s, repair, c.blocked, &nr, &c.rgrid)) return GGEMM_ERR_NUMERICS;
+    if (recon_launch(doz, dyd, c.ne, c.max_m, c.max_n, s, repair, c.blocked, &nr, &c.rgrid, c.dot_form))
+      return GGEMM_ERR_NUMERICS;
     *launches += nr;
     prof::mark(prof_set, 3, s);
   } else {
@@ -555,7 +557,7 @@ int path_emu_loop(ggemm_handle_t h, bool batched, const ggemm_problem_t* probs, 
     }
     q += planes;
     int nr = 0;
-    if (recon_launch(doz + j, dyd + j, 1, hoz[j].m, hoz[j].n, h->stream, repair, c.blocked, &nr)) {
+    if (recon_launch(doz + j, dyd + j, 1, hoz[j].m, hoz[j].n, h->stream, repair, c.blocked, &nr, nullptr, c.dot_form)) {
       r = GGEMM_ERR_NUMERICS;
       break;
     }
@@ -748,6 +750,12 @@ extern "C" int ggemm_create_ex(ggemm_handle_t* out, int max_problems, size_t max
   h->packed_max_kp = epk ? std::max(0, std::atoi(epk)) : kPackedMaxKp;
   const char* esf = std::getenv("GGEMM_SAFETY_CHAINS");
   h->safety_chains = (esf && std::atoi(esf) == 1) ? 1 : 0;
+  const char* edf = std::getenv("GGEMM_DOT_FORM");
+  h->dot_form = !edf                          ? kDotFormAuto
+                : !std::strcmp(edf, "dense")  ? kDotFormDense
+                : !std::strcmp(edf, "blocks") ? kDotFormBlocks
+                : !std::strcmp(edf, "list")   ? kDotFormList
+                                              : kDotFormAuto;
   if (hipStreamSynchronize(stream) != hipSuccess) FAIL(GGEMM_ERR_CUDA);
 #undef HIPA
 #undef FAIL

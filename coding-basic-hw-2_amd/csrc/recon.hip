@@ -489,6 +489,9 @@ __global__ void __launch_bounds__(kThreads) recon_kernel(const oz2_problem* __re
 //     chains of the tile at once, each thread a 4 x 4 register block (16 chains), the k-chunks of
 //     A (64 rows) and B (64 columns) double-buffered in LDS and read as 32-byte row / column
 //     quads that a wave's lanes share (broadcast reads): 4 LDS reads per 16 fmas;
+//   * compact: when the flagged entries lie in nR rows and nC columns with nR nC <= kCompactMax,
+//     the workgroup stages those rows of A and columns of B once per k-chunk and runs the nR nC
+//     chains of their crossings, one per thread (compact_dots);
 //   * per block: a block with flagged entries in at least kWaveDots lanes takes them all with 4
 //     chains per lane (wave_dots: wave w the blocks of block column w);
 //   * sparse: the remaining entries go to a per-workgroup list; for up to 16 entries at a time
@@ -502,6 +505,7 @@ constexpr int kDenseMin = 1024;    // flagged entries of a tile from which it ta
 constexpr int kDK = 8;             // dense k-chunk
 constexpr int kSG = 16;            // sparse: entries per group
 constexpr int kListCap = 256;      // sparse list capacity (16 blocks x 3 lanes x 4 entries fit)
+constexpr int kCompactMax = 256;   // compact form: rows x columns of the flagged entries, one chain per thread
 constexpr int kWaveLds = 16 * kKC + 16 * (kKC + 1);   // doubles of one wave's wave_dots staging
 constexpr int kUnion = 4 * kWaveLds;                  // wave_dots x 4 waves; >= dense, sparse
 static_assert(4 * kDK * kRT <= kUnion && 2 * 1024 <= kUnion, "dot-pass LDS union");
@@ -550,6 +554,11 @@ __device__ __forceinline__ bool nf_dot(const oz2_problem& pr, const GLOBAL int32
   if (!(nan || pos || neg)) return false;   // no infinity listed (not a safety entry)
   d = (nan || (pos && neg)) ? __builtin_nan("") : (pos ? __builtin_inf() : -__builtin_inf());
   return true;
+}
+
+__device__ __forceinline__ unsigned long long uniform_u64(unsigned long long v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return ((unsigned long long)hi << 32) | lo;
 }
 
 // Flagged entries of the tile counted into *c (threads 0 .. 63 read one flag word each).
@@ -652,6 +661,96 @@ __device__ __forceinline__ void dense_dots(const oz2_problem& pr, int r0, int c0
   }
 }
 
+// The chains of the crossings of nR tile rows (rmap) and nC tile columns (cmap), nR nC <= kCompactMax:
+// thread t < nR nC runs the chain of row rmap[t / nC], column cmap[t % nC] and stores it if that
+// entry is flagged.  Per k-chunk of KC (the largest power of two with nRp + nC rows of KC + 2
+// doubles in the LDS union and at most 6 staging loads per thread; nRp = nR rounded up to a power
+// of two) the rows of A are staged with consecutive threads on consecutive rows (A is column-major)
+// and the columns of B with consecutive threads on consecutive k, the next chunk's loads in flight
+// while the chains run; a chain reads its row and column two k at a time (16-byte LDS reads; KC + 2
+// is even).
+__device__ __forceinline__ void compact_dots(const oz2_problem& pr, int r0, int c0, const uint64_t* fl,
+                                             const uint8_t* rmap, const uint8_t* cmap, int nR, int nC,
+                                             double* buf) {
+  const GLOBAL double* A = gp(pr.A);
+  const GLOBAL double* B = gp(pr.B);
+  const size_t lda = (size_t)pr.lda, ldb = (size_t)pr.ldb;
+  const int K = pr.k;
+  const int t = threadIdx.x;
+  const int lr = nR > 1 ? 32 - __clz(nR - 1) : 0;   // nRp = 2^lr >= nR
+  const int nq = (1 << lr) + nC;
+  const int kcap = min(kUnion / nq - 2, 6 * kThreads / nq);
+  const int lg = 31 - __clz(kcap);   // KC = 2^lg <= kcap
+  const int KC = 1 << lg, S = KC + 2;
+  const int nA = KC << lr, nS = nq * KC;   // staging elements: A rows (padded to nRp), B columns
+  constexpr int NS = 6;   // staging loads per thread (8 would cost the kernel its fifth wave per SIMD)
+  double v[NS];
+  auto fetch = [&](int kc) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const int x = t + kThreads * s;
+      if (x < nA) {
+        const int q = x & ((1 << lr) - 1), kk = x >> lr;
+        if (q < nR) v[s] = A[(size_t)(r0 + rmap[q]) + (size_t)min(kc + kk, K - 1) * lda];
+      } else if (x < nS) {
+        const int y = x - nA, q = y >> lg, kk = y & (KC - 1);
+        v[s] = B[(size_t)min(kc + kk, K - 1) + (size_t)(c0 + cmap[q]) * ldb];
+      }
+    }
+  };
+  auto put = [&]() {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const int x = t + kThreads * s;
+      if (x < nA) {
+        const int q = x & ((1 << lr) - 1);
+        if (q < nR) buf[q * S + (x >> lr)] = v[s];
+      } else if (x < nS) {
+        const int y = x - nA;
+        buf[(nR + (y >> lg)) * S + (y & (KC - 1))] = v[s];
+      }
+    }
+  };
+  const bool act = t < nR * nC;
+  const int cr = act ? t / nC : 0, cc = act ? t - cr * nC : 0;
+  const double* a_ = buf + cr * S;
+  const double* b_ = buf + (nR + cc) * S;
+  double acc = 0.0;
+  if (K > 0) {
+    fetch(0);
+    put();
+  }
+  lds_sync();
+  for (int kc = 0; kc < K; kc += KC) {
+    const int kn = min(KC, K - kc);
+    const bool more = kc + KC < K;
+    if (more) fetch(kc + KC);   // in flight while the chains run
+    if (act) {
+      int kk = 0;
+#pragma unroll 2
+      for (; kk + 2 <= kn; kk += 2) {
+        const v2d a2 = *reinterpret_cast<const v2d*>(a_ + kk);
+        const v2d b2 = *reinterpret_cast<const v2d*>(b_ + kk);
+        acc = fma(a2.x, b2.x, acc);
+        acc = fma(a2.y, b2.y, acc);
+      }
+      if (kk < kn) acc = fma(a_[kk], b_[kk], acc);
+    }
+    lds_sync();   // every chain done with this chunk
+    if (more) {
+      put();
+      lds_sync();
+    }
+  }
+  if (act) {
+    const int il = rmap[cr], jl = cmap[cc];
+    if (tile_flag(fl, il, jl)) {
+      GLOBAL double* cp = gpw(pr.C) + (size_t)(r0 + il) + (size_t)(c0 + jl) * pr.ldc;
+      *cp = from_dot(pr.alpha, pr.beta, acc, pr.beta != 0.0 ? *cp : 0.0);
+    }
+  }
+}
+
 // The listed entries (tile-local row / column, packed 16 + 16 bits) in groups of at most kSG: lane e
 // of the group runs entry e's chain; all threads stage the group's A rows and B columns through LDS
 // in k-chunks of 1024 / (group size rounded up to a power of two) -- 4 loads of A and 4 of B per
@@ -719,12 +818,15 @@ __device__ __forceinline__ void sparse_dots(const oz2_problem& pr, int r0, int c
   }
 }
 
-__global__ void __launch_bounds__(kThreads) dots_kernel(const oz2_problem* __restrict__ probs,
-                                                        const YDesc* __restrict__ yds, int gne, int gper) {
+// (launch bounds: five waves per SIMD, which the chains' latency needs)
+__global__ void __launch_bounds__(kThreads, 5) dots_kernel(const oz2_problem* __restrict__ probs,
+                                                        const YDesc* __restrict__ yds, int gne, int gper, int form) {
   __shared__ __attribute__((aligned(16))) double buf[kUnion];
   __shared__ uint64_t fl[64];       // flag words of the tile's 16 blocks (4 per block, column-major blocks)
   __shared__ uint32_t list[kListCap];
   __shared__ int cnt[2];            // flagged entries of the tile, listed entries
+  __shared__ unsigned long long rcm[2];   // tile rows / columns holding flagged entries
+  __shared__ uint8_t rmap[kRT], cmap[kRT];
   int pi, lt;
   grid_tile<true>(yds, gne, gper, pi, lt);
   const oz2_problem& pr = probs[pi];
@@ -740,7 +842,10 @@ __global__ void __launch_bounds__(kThreads) dots_kernel(const oz2_problem* __res
   if (t < 64) {   // word t % 4 of block t / 4 = (bi, bj) = (t / 4 % 4, t / 16)
     const int bi = (r0 >> 4) + ((t >> 2) & 3), bj = (c0 >> 4) + (t >> 4);
     fl[t] = (bi < mb && bj * 16 < n) ? gp(yds[pi].F)[4 * ((size_t)bj * mb + bi) + (t & 3)] : 0ull;
-    if (t == 0) cnt[1] = 0;
+    if (t == 0) {
+      cnt[1] = 0;
+      rcm[0] = rcm[1] = 0ull;
+    }
   }
   count_flags(fl, &cnt[0]);
   lds_sync();
@@ -794,8 +899,32 @@ __global__ void __launch_bounds__(kThreads) dots_kernel(const oz2_problem* __res
     total = cnt[0];
     if (total == 0) return;   // workgroup-uniform
   }
-  if (total >= kDenseMin) {
+  if (form == kDotFormDense || (form == kDotFormAuto && total >= kDenseMin)) {
     dense_dots(pr, r0, c0, fl, buf);
+    return;
+  }
+  if (form == kDotFormAuto && t < 64) {   // rows and columns of the flagged entries: word t covers rows 16 bi + 4 q + e, columns 16 bj + c
+    const uint64_t v = fl[t];
+    const int bi = (t >> 2) & 3, bj = t >> 4, e = t & 3;
+    unsigned long long rb = 0ull;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if ((v >> (16 * q)) & 0xffffull) rb |= 1ull << (16 * bi + 4 * q + e);
+    const unsigned long long cbits = ((v | (v >> 16) | (v >> 32) | (v >> 48)) & 0xffffull) << (16 * bj);
+    if (rb) atomicOr(&rcm[0], rb);
+    if (cbits) atomicOr(&rcm[1], cbits);
+  }
+  lds_sync();
+  // workgroup-uniform: moved to scalar registers, and everything derived from them with them
+  const unsigned long long rmask = uniform_u64(rcm[0]), cmask = uniform_u64(rcm[1]);
+  const int nR = __popcll(rmask), nC = __popcll(cmask);
+  if (form == kDotFormAuto && nR * nC <= kCompactMax) {   // workgroup-uniform
+    if (t < 64) {
+      if ((rmask >> t) & 1ull) rmap[__popcll(rmask & ((1ull << t) - 1ull))] = (uint8_t)t;
+      if ((cmask >> t) & 1ull) cmap[__popcll(cmask & ((1ull << t) - 1ull))] = (uint8_t)t;
+    }
+    lds_sync();
+    compact_dots(pr, r0, c0, fl, rmap, cmap, nR, nC, buf);
     return;
   }
   const int j = c0 + 16 * w + (lane & 15);
@@ -805,7 +934,7 @@ __global__ void __launch_bounds__(kThreads) dots_kernel(const oz2_problem* __res
 #pragma unroll
     for (int e = 0; e < 4; ++e) dm |= (unsigned)((fl[4 * (4 * w + bi) + e] >> lane) & 1u) << e;
     GLOBAL double* const cp = gpw(pr.C) + (dm ? i0 + (size_t)j * pr.ldc : 0);
-    if (__popcll(__ballot(dm != 0u)) >= kWaveDots) {   // wave-uniform
+    if (form != kDotFormList && __popcll(__ballot(dm != 0u)) >= kWaveDots) {   // wave-uniform
       double acc[4];
       wave_dots(pr, r0 + 16 * bi, c0 + 16 * w, lane, buf + w * kWaveLds, buf + w * kWaveLds + 16 * kKC, acc);
 #pragma unroll
@@ -829,7 +958,7 @@ __global__ void __launch_bounds__(kThreads) dots_kernel(const oz2_problem* __res
 }  // namespace
 
 int recon_launch(const oz2_problem* d, const YDesc* yd, int num, int max_m, int max_n, hipStream_t s, int mode,
-                 bool blocked, int* launches, const ReconGrid* grid) {
+                 bool blocked, int* launches, const ReconGrid* grid, int dot_form) {
   if (launches) *launches = 0;
   if (num <= 0) return 0;
   if (mode != OZ2_REPAIR_OFF && mode != OZ2_REPAIR_COUNT && mode != OZ2_REPAIR_ON) return 1;
@@ -864,7 +993,7 @@ int recon_launch(const oz2_problem* d, const YDesc* yd, int num, int max_m, int 
     ++nl;
   }
   if (blk && gd > 0) {
-    hipLaunchKernelGGL(dots_kernel, dim3((unsigned)gd, gy), dim3(kThreads), 0, s, d, yd, gne, dper);
+    hipLaunchKernelGGL(dots_kernel, dim3((unsigned)gd, gy), dim3(kThreads), 0, s, d, yd, gne, dper, dot_form);
     ++nl;
   }
   if (launches) *launches = nl;

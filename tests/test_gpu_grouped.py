@@ -404,16 +404,19 @@ def env_handle(case, min_k=None, **env):
         os.environ.update(saved)
 
 
+@pytest.mark.parametrize("form", ["auto", "dense", "blocks", "list"])
 @pytest.mark.parametrize("chains", [True, False])
 @pytest.mark.parametrize("k", [5, 16, 17, 40, 333])
-def test_dense_and_sparse_dot_forms(k, chains):
-    """The reconstruct's FP64 dot-product forms against the oracle's chains, bit for bit, COUNT and
-    ON: tiles whose NaN / Inf rows and columns put more than a quarter of their entries on the safety
-    fallback (dense form, k-chunks of 16 with a partial last chunk for k % 16 != 0 and a single
-    partial chunk for k < 16), tiles with a few such rows (per-block form), and repairs scattered
-    over clean tiles (per-workgroup list); ragged m, n, alpha != 1, beta != 0.  chains: the safety
-    entries run their fma chains (GGEMM_SAFETY_CHAINS=1), which is what puts tiles on the dense
-    and per-block forms; else they are decided from prep's non-finite summaries."""
+def test_dense_and_sparse_dot_forms(k, chains, form):
+    """The dot-product pass's forms against the oracle's chains, bit for bit, COUNT and ON: tiles
+    whose NaN / Inf rows and columns put more than a quarter of their entries on the safety fallback
+    (dense form: k-chunks with a partial last chunk for k % 8 != 0 and a single partial chunk for
+    k < 8), tiles with a few such rows (compact form, or per block), and repairs scattered over clean
+    tiles (compact form, or the per-workgroup list); ragged m, n, alpha != 1, beta != 0.  chains: the
+    safety entries run their fma chains (GGEMM_SAFETY_CHAINS=1), else they are decided from prep's
+    non-finite summaries.  form (GGEMM_DOT_FORM): the automatic choice, or every flagged tile dense,
+    per-block and listed entries only, listed entries only (more than the list holds: per-lane
+    chains)."""
     shapes = [(70, 130, k, -1.5, 0.75), (130, 70, k, 2.0, -0.5), (64, 64, k, 1.0, 0.0), (200, 17, k, 0.5, 1.0)]
     case = Case(shapes, 20261216 + k, phi=3.0)
     rng = np.random.default_rng(k)
@@ -430,9 +433,12 @@ def test_dense_and_sparse_dot_forms(k, chains):
         h.B[int(rng.integers(0, k)) + c * h.ldb] = np.nan
     case.alloc()
     for mode in (G.REPAIR_COUNT, G.REPAIR_ON):
-        say(f"dot forms k={k} mode={mode} chains={chains}")
+        say(f"dot forms k={k} mode={mode} chains={chains} form={form}")
         cfg = G.Config(0, 1e-15, 1, mode)
-        with env_handle(case, min_k=1, GGEMM_SAFETY_CHAINS="1" if chains else "0") as hd:
+        env = {"GGEMM_SAFETY_CHAINS": "1" if chains else "0"}
+        if form != "auto":
+            env["GGEMM_DOT_FORM"] = form
+        with env_handle(case, min_k=1, **env) as hd:
             rc, st = run(case, G.PATH_EMU_GROUPED, cfg, handle=hd)
         assert rc == 0
         tot = check_case(case, G.PATH_EMU_GROUPED, cfg, st, O.REPAIR_ON if mode == G.REPAIR_ON else O.REPAIR_COUNT)
