@@ -10,9 +10,10 @@ namespace ggemm {
 //   [F64 schedule(s)][INT8 schedule(s)]
 // every section 256-byte aligned; the INT8 schedule is last so the H2D can stop at its used size.
 struct BlobLayout {
-  size_t off_oz, off_yd, off_prep, off_i8, off_epi, off_f64, off_sf64, off_si8, total;
+  size_t off_oz, off_yd, off_prep, off_po, off_i8, off_epi, off_f64, off_sf64, off_si8, total;
 };
 // nprep: prep descriptors of operand reuse (unique A, then unique B), 0 without reuse
+// off_po: the prep launch's problem order (ne + nprep ints; see prep_launch)
 BlobLayout layout_for(size_t ne, size_t nprep, size_t n_i8, size_t nn, size_t sched_f64, size_t sched_i8);
 inline size_t sched_img(int entries) { return align_up(sched_bytes(entries), kBufAlign); }
 

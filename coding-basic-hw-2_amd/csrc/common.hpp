@@ -195,8 +195,9 @@ int f64_launch(const F64Problem* d_probs, const void* d_sched, int launch, hipSt
 // fold_q: A residues carry the CRT inverses (production); packed: residue planes in the packed layout
 // max_moduli: the largest num_moduli among the num problems (selects the digit width)
 // yd (or nullptr): descriptors parallel to d whose nf summaries prep writes
+// order (or nullptr: 0 .. num - 1): the problems in the order their workgroups are dispatched
 int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t s, int fold_q, int packed,
-                int max_moduli, const YDesc* yd = nullptr);
+                int max_moduli, const YDesc* yd = nullptr, const int* order = nullptr);
 // yd == nullptr: read the int32 planes of oz2_problem::C32 (kernel-level API); else the digits.
 // blocked: the digits and L of every problem are in the blocked layout (production, yd != nullptr);
 // the reconstruct then flags the entries that take FP64 dot products and a second kernel computes

@@ -613,10 +613,12 @@ template <bool kWide>
 __global__ void __launch_bounds__(kThreads, 4) prep_kernel(const oz2_problem* __restrict__ probs, int a_blocks,
                                                         const CrtTables* __restrict__ tab,
                                                         unsigned long long* __restrict__ cnt, int fold_q,
-                                                        int packed, const YDesc* __restrict__ yds) {
+                                                        int packed, const YDesc* __restrict__ yds,
+                                                        const int* __restrict__ order) {
   __shared__ PrepShared sm;
-  const oz2_problem& pr = probs[blockIdx.y];
-  int32_t* const nfo = yds ? yds[blockIdx.y].nf : nullptr;
+  const int pi = order ? order[blockIdx.y] : (int)blockIdx.y;
+  const oz2_problem& pr = probs[pi];
+  int32_t* const nfo = yds ? yds[pi].nf : nullptr;
   const int N = pr.num_moduli;
   if (N < 1 || N > kMaxModuli || pr.alpha == 0.0) return;   // alpha == 0: A, B never referenced
   // folded A residues use the weights q 2^(8 i) mod p, so that sum b_i [q 2^(8 i)] = q x (mod p)
@@ -635,7 +637,7 @@ int g_force_split = 0;
 }  // namespace
 
 int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t s, int fold_q, int packed,
-                int max_moduli, const YDesc* yd) {
+                int max_moduli, const YDesc* yd, const int* order) {
   if (num <= 0) return 0;
   if (num > 65535 || max_m < 0 || max_n < 0 || max_moduli < 1 || max_moduli > kMaxModuli) return 1;
   DevCtx* c = dev_ctx();
@@ -651,10 +653,10 @@ int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t
   if (!ht) return 2;
   if (ht->T[max_moduli] < 0x1.8p62)
     hipLaunchKernelGGL(prep_kernel<false>, dim3(a_blocks + b_blocks, num, S), dim3(kThreads), 0, s, d, a_blocks,
-                       c->tab, c->counters, fold_q, packed, yd);
+                       c->tab, c->counters, fold_q, packed, yd, order);
   else
     hipLaunchKernelGGL(prep_kernel<true>, dim3(a_blocks + b_blocks, num, S), dim3(kThreads), 0, s, d, a_blocks,
-                       c->tab, c->counters, fold_q, packed, yd);
+                       c->tab, c->counters, fold_q, packed, yd, order);
   return hipGetLastError() == hipSuccess ? 0 : 3;
 }
 
