@@ -13,7 +13,7 @@ struct BlobLayout {
   size_t off_oz, off_yd, off_prep, off_po, off_i8, off_epi, off_f64, off_sf64, off_si8, total;
 };
 // nprep: prep descriptors of operand reuse (unique A, then unique B), 0 without reuse
-// off_po: the prep launch's problem order (ne + nprep ints; see prep_launch)
+// off_po: the prep launch's problem order, then its block offsets (2 (ne + nprep) ints; see prep_launch)
 BlobLayout layout_for(size_t ne, size_t nprep, size_t n_i8, size_t nn, size_t sched_f64, size_t sched_i8);
 inline size_t sched_img(int entries) { return align_up(sched_bytes(entries), kBufAlign); }
 
@@ -33,6 +33,7 @@ struct GroupedCall {
   int f64_tiles = 0;              // native GEMM launch word (tile count, kF64Tile128 for 128 x 128 tiles)
   ReconGrid rgrid{};              // compact reconstruct / dot-product grids
   int dot_form = 0;               // the handle's dot-product form override (kDotForm*)
+  long long prep_blocks = 0;      // workgroups of the compact prep grid (per split)
   size_t h2d_bytes = 0;           // bytes of the blob to copy
 };
 

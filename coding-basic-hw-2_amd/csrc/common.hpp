@@ -180,6 +180,8 @@ struct ReconGrid {
 // Reconstruct tile shapes (rows x columns per workgroup): blocked digits / column-major, and the
 // dot-product pass's tile
 constexpr int kReconTileMB = 64, kReconTileNB = 16, kReconTileMC = 128, kReconTileNC = 8, kDotTile = 64;
+// Prep workgroup shapes: rows of A per A-row block, columns of B per B-column block
+constexpr int kPrepRows = 32, kPrepCols = 8;
 
 // FP64 MFMA grouped GEMM (native routes).  h_ws receives the schedule image; *launch receives the
 // launch word for f64_launch: the tile count in bits 0-29, kF64Tile128 set for 128 x 128 tiles (0:
@@ -196,8 +198,12 @@ int f64_launch(const F64Problem* d_probs, const void* d_sched, int launch, hipSt
 // max_moduli: the largest num_moduli among the num problems (selects the digit width)
 // yd (or nullptr): descriptors parallel to d whose nf summaries prep writes
 // order (or nullptr: 0 .. num - 1): the problems in the order their workgroups are dispatched
+// pofs (with order, or nullptr): a compact grid of total_blocks workgroups, problem order[i] owning
+// blocks pofs[i] .. pofs[i + 1] - 1 (ceil(m / 32) A-row blocks, then ceil(n / 8) B-column blocks;
+// none for problems prep skips)
 int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t s, int fold_q, int packed,
-                int max_moduli, const YDesc* yd = nullptr, const int* order = nullptr);
+                int max_moduli, const YDesc* yd = nullptr, const int* order = nullptr, const int* pofs = nullptr,
+                long long total_blocks = 0);
 // yd == nullptr: read the int32 planes of oz2_problem::C32 (kernel-level API); else the digits.
 // blocked: the digits and L of every problem are in the blocked layout (production, yd != nullptr);
 // the reconstruct then flags the entries that take FP64 dot products and a second kernel computes

@@ -64,7 +64,7 @@ BlobLayout layout_for(size_t ne, size_t nprep, size_t n_i8, size_t nn, size_t sc
   L.off_yd = align_up(ne * sizeof(oz2_problem), kBufAlign);
   L.off_prep = align_up(L.off_yd + ne * sizeof(YDesc), kBufAlign);
   L.off_po = align_up(L.off_prep + nprep * sizeof(oz2_problem), kBufAlign);
-  L.off_i8 = align_up(L.off_po + (ne + nprep) * sizeof(int), kBufAlign);
+  L.off_i8 = align_up(L.off_po + 2 * (ne + nprep) * sizeof(int), kBufAlign);
   L.off_epi = align_up(L.off_i8 + n_i8 * sizeof(i8_problem), kBufAlign);
   L.off_f64 = align_up(L.off_epi + n_i8 * sizeof(I8Epi), kBufAlign);
   L.off_sf64 = align_up(L.off_f64 + nn * sizeof(F64Problem), kBufAlign);
@@ -354,6 +354,18 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
     for (int i = 0; i < np; ++i) po[i] = i;
     auto vol = [&](int i) { return ((long long)pd[i].m + pd[i].n) * pd[i].kp; };
     std::stable_sort(po, po + np, [&](int a, int b) { return vol(a) > vol(b); });
+    // compact grid: each problem's first block, in dispatch order (problems prep skips get none)
+    int* pof = po + np;
+    long long tot = 0;
+    for (int i = 0; i < np; ++i) {
+      const oz2_problem& o = pd[po[i]];
+      if (tot > 0x7fffffffLL) return GGEMM_ERR_INVALID;
+      pof[i] = (int)tot;
+      if (o.alpha != 0.0 && o.num_moduli >= 1 && o.num_moduli <= kMaxModuli)
+        tot += (long long)(o.m + kPrepRows - 1) / kPrepRows + (o.n + kPrepCols - 1) / kPrepCols;
+    }
+    if (tot > 0x7fffffffLL) return GGEMM_ERR_INVALID;
+    c.prep_blocks = tot;
   }
   for (int i = 0; i < c.nn; ++i) hf[i] = f64_of(probs[nat_idx[i]]);
   if (c.nn && f64_build_schedule(hf, c.nn, hb + c.L.off_sf64, s_f64, &c.f64_tiles, nullptr, h->f64_tile))
@@ -374,7 +386,8 @@ int enqueue_grouped(const GroupedCall& c, const char* db, hipStream_t s, int rep
     const bool shared = c.nprep > 0;   // operand reuse: prep once per unique operand
     if (prep_launch(shared ? reinterpret_cast<const oz2_problem*>(db + c.L.off_prep) : doz, shared ? c.nprep : c.ne,
                     shared ? c.pmax_m : c.max_m, shared ? c.pmax_n : c.max_n, s, 1, c.packed, c.nmax,
-                    shared ? nullptr : dyd, reinterpret_cast<const int*>(db + c.L.off_po)))
+                    shared ? nullptr : dyd, reinterpret_cast<const int*>(db + c.L.off_po),
+                    reinterpret_cast<const int*>(db + c.L.off_po) + (shared ? c.nprep : c.ne), c.prep_blocks))
       return GGEMM_ERR_NUMERICS;
     ++*launches;
     prof::mark(prof_set, 1, s);

@@ -49,6 +49,7 @@ constexpr int kARows = 32;      // rows of A per block
 constexpr int kATile = 128;     // k tile of the A residue pass
 constexpr int kBCols = 8;       // columns of B per block (32 lanes each)
 constexpr int kChains = 8;      // A-row reduction chains
+static_assert(kARows == kPrepRows && kBCols == kPrepCols, "prep block shapes");
 
 __device__ __forceinline__ double pow2d(int e) {   // 2^e, e in [-1022, 1023]
   return __longlong_as_double((long long)(e + 1023) << 52);
@@ -608,22 +609,38 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
 }
 
 // kWide: three-word digits (any N); the two-word kernel is launched only for calls whose every
-// problem has T_N < 1.5 2^62
+// problem has T_N < 1.5 2^62.
+// Grid: compact (pofs != nullptr) -- blockIdx.x runs over the real blocks of all problems, problem
+// order[i] owning blocks pofs[i] .. pofs[i + 1] - 1, its A-row blocks first; else blockIdx.y is the
+// problem (through order when given) and blockIdx.x one of a_blocks A-row blocks or a B-column
+// block, as wide as the largest problem.
 template <bool kWide>
 __global__ void __launch_bounds__(kThreads, 4) prep_kernel(const oz2_problem* __restrict__ probs, int a_blocks,
                                                         const CrtTables* __restrict__ tab,
                                                         unsigned long long* __restrict__ cnt, int fold_q,
                                                         int packed, const YDesc* __restrict__ yds,
-                                                        const int* __restrict__ order) {
+                                                        const int* __restrict__ order, const int* __restrict__ pofs,
+                                                        int nprob) {
   __shared__ PrepShared sm;
-  const int pi = order ? order[blockIdx.y] : (int)blockIdx.y;
+  int pi, blk = (int)blockIdx.x;
+  if (pofs) {   // the last problem whose first block is at most blockIdx.x (empty problems are skipped)
+    int lo = 0, hi = nprob - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (pofs[mid] <= blk) lo = mid; else hi = mid - 1;
+    }
+    pi = order[lo];
+    blk -= pofs[lo];
+    a_blocks = (probs[pi].m + kARows - 1) / kARows;
+  } else {
+    pi = order ? order[blockIdx.y] : (int)blockIdx.y;
+  }
   const oz2_problem& pr = probs[pi];
   int32_t* const nfo = yds ? yds[pi].nf : nullptr;
   const int N = pr.num_moduli;
   if (N < 1 || N > kMaxModuli || pr.alpha == 0.0) return;   // alpha == 0: A, B never referenced
   // folded A residues use the weights q 2^(8 i) mod p, so that sum b_i [q 2^(8 i)] = q x (mod p)
-  const bool fold = fold_q && (int)blockIdx.x < a_blocks;
-  const int blk = (int)blockIdx.x;
+  const bool fold = fold_q && blk < a_blocks;
   if (blk < a_blocks) {
     if (blk * kARows >= pr.m) return;
     prep_rows<kWide>(pr, tab, blk, blockIdx.z, gridDim.z, sm, cnt, fold ? N : 0, packed != 0, nfo);
@@ -637,26 +654,30 @@ int g_force_split = 0;
 }  // namespace
 
 int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t s, int fold_q, int packed,
-                int max_moduli, const YDesc* yd, const int* order) {
+                int max_moduli, const YDesc* yd, const int* order, const int* pofs, long long total_blocks) {
   if (num <= 0) return 0;
   if (num > 65535 || max_m < 0 || max_n < 0 || max_moduli < 1 || max_moduli > kMaxModuli) return 1;
+  if (pofs && (!order || total_blocks < 0 || total_blocks > 0x7fffffffLL)) return 1;
   DevCtx* c = dev_ctx();
   if (!c) return 2;
   const int a_blocks = (max_m + kARows - 1) / kARows;
   const int b_blocks = (max_n + kBCols - 1) / kBCols;
   if (a_blocks + b_blocks == 0) return 0;
-  const long long blocks = (long long)(a_blocks + b_blocks) * num;
+  const long long blocks = pofs ? total_blocks : (long long)(a_blocks + b_blocks) * num;
+  if (blocks == 0) return 0;
+  const dim3 grid = pofs ? dim3((unsigned)blocks, 1, 1) : dim3(a_blocks + b_blocks, num, 1);
   const long long target = 4LL * c->num_cus;
   int S = (int)std::min<long long>(16, std::max<long long>(1, (target + blocks - 1) / blocks));
   if (g_force_split > 0) S = g_force_split;
   const CrtTables* ht = host_tables();
   if (!ht) return 2;
+  const dim3 g3(grid.x, grid.y, S);
   if (ht->T[max_moduli] < 0x1.8p62)
-    hipLaunchKernelGGL(prep_kernel<false>, dim3(a_blocks + b_blocks, num, S), dim3(kThreads), 0, s, d, a_blocks,
-                       c->tab, c->counters, fold_q, packed, yd, order);
+    hipLaunchKernelGGL(prep_kernel<false>, g3, dim3(kThreads), 0, s, d, a_blocks, c->tab, c->counters, fold_q, packed,
+                       yd, order, pofs, num);
   else
-    hipLaunchKernelGGL(prep_kernel<true>, dim3(a_blocks + b_blocks, num, S), dim3(kThreads), 0, s, d, a_blocks,
-                       c->tab, c->counters, fold_q, packed, yd, order);
+    hipLaunchKernelGGL(prep_kernel<true>, g3, dim3(kThreads), 0, s, d, a_blocks, c->tab, c->counters, fold_q, packed,
+                       yd, order, pofs, num);
   return hipGetLastError() == hipSuccess ? 0 : 3;
 }
 
