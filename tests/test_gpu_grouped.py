@@ -222,6 +222,14 @@ def test_uniform_group_beta(path):
     check_case(case, path, cfg, st, O.REPAIR_ON if path == G.PATH_AUTO else O.REPAIR_COUNT)
 
 
+def ran_kernel(name, env=None):
+    """The INT8 kernel the last call ran is `name`, or its persistent form when the persistent
+    schedule is selected for the handle (env) or for the whole process."""
+    sched = (env or {}).get("GGEMM_I8_SCHED", os.environ.get("GGEMM_I8_SCHED"))
+    want = name.replace("_kernel", "_persistent_kernel") if sched == "persistent" else name
+    return G.lib().ggemm_profile_i8_kernel().decode() == want
+
+
 def kernel_handle(case, kernel=None, **env):
     """A handle created with GGEMM_I8_KERNEL (and further variables) set: read at creation."""
     saved = dict(os.environ)
@@ -240,10 +248,7 @@ def run_kernel(case, kernel, cfg=CFG_EMU, **env):
     with kernel_handle(case, kernel, **env) as h:
         rc, st = run(case, G.PATH_EMU_GROUPED, cfg, handle=h)
         assert rc == 0
-        want = {"large": "i8_large_kernel", "general": "i8_grouped_kernel"}[kernel]
-        if env.get("GGEMM_I8_SCHED") == "persistent":
-            want = want.replace("_kernel", "_persistent_kernel")
-        assert G.lib().ggemm_profile_i8_kernel().decode() == want
+        assert ran_kernel({"large": "i8_large_kernel", "general": "i8_grouped_kernel"}[kernel], env)
         check_case(case, G.PATH_EMU_GROUPED, cfg, st, O.REPAIR_COUNT, blocked=env.get("GGEMM_DIGITS_COLMAJOR") != "1")
         return [case.C(g).copy() for g in range(len(case.hp))]
 
@@ -300,7 +305,7 @@ def test_default_kernel_choice():
     short = Case([(256, 256, 300)] * 2, 20261209, phi=0.5)
     with kernel_handle(short) as h:
         rc, st = run(short, G.PATH_EMU_GROUPED, CFG_EMU, handle=h)
-        assert rc == 0 and G.lib().ggemm_profile_i8_kernel().decode() == "i8_grouped_kernel"
+        assert rc == 0 and ran_kernel("i8_grouped_kernel")
     props = torch.cuda.get_device_properties(0)
     g = (props.multi_processor_count + 3) // 4      # 4 tiles of 256 x 256 per problem
     long_k = Case([(512, 512, 4128)] * g, 20261210, phi=0.5)   # kp = 4128 > 4096: row-major
@@ -308,7 +313,7 @@ def test_default_kernel_choice():
     for kernel, name in ((None, "i8_large_kernel"), ("general", "i8_grouped_kernel")):
         with kernel_handle(long_k, kernel) as h:
             rc, st = run(long_k, G.PATH_EMU_GROUPED, CFG_EMU, handle=h)
-            assert rc == 0 and G.lib().ggemm_profile_i8_kernel().decode() == name
+            assert rc == 0 and ran_kernel(name)
             outs.append([long_k.C(q).copy() for q in range(g)])
     for a, b in zip(*outs):   # the oracle checks both kernels on smaller shapes above
         assert same_bits(a, b)
@@ -330,7 +335,7 @@ def test_default_layout_long_k_matches_oracle():
         say(f"long-k default layout, kernel {name}")
         with kernel_handle(case, kernel) as h:
             rc, st = run(case, G.PATH_EMU_GROUPED, cfg, handle=h)
-            assert rc == 0 and G.lib().ggemm_profile_i8_kernel().decode() == name
+            assert rc == 0 and ran_kernel(name)
         assert (st.moduli_min, st.moduli_max, st.kernel_launches) == (15, 16, 2 + recon_launches())
         for g, (Co, cnt) in enumerate(want):
             assert same_bits(case.C(g), Co), f"{name}: problem {g} differs"
