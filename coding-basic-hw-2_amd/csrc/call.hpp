@@ -29,7 +29,8 @@ struct GroupedCall {
   i8_sched_info i8info{};
   int i8_kernel = kI8General;     // INT8 GEMM kernel the schedule was built for
   bool blocked = false;           // digit and abs planes in the blocked layout
-  bool packed = false;            // residue planes in the packed layout
+  bool packed = false;            // every problem's residue planes in the packed layout
+  int packed_kp = 0;              // problems with Kp at most this (> 0) use the packed layout
   int f64_tiles = 0;              // native GEMM launch word (tile count, kF64Tile128 for 128 x 128 tiles)
   ReconGrid rgrid{};              // compact reconstruct / dot-product grids
   int dot_form = 0;               // the handle's dot-product form override (kDotForm*)

@@ -112,7 +112,7 @@ __host__ __device__ inline int i8_tile_n(int cfg) { return cfg == 0 ? 128 : (cfg
 // consecutive rows is then one contiguous span.
 enum : uint32_t { kEpiResidue = 1u, kEpiBlocked = 2u, kEpiPacked = 4u, kEpiAccBias = 8u };
 constexpr int kAccBiasMaxKp = 32768;   // |C| <= 128^2 kp <= 2^29
-constexpr int kPackedMaxKp = 4096;   // production calls whose largest Kp is at most this use packing
+constexpr int kPackedMaxKp = 4096;   // production problems whose Kp is at most this use packing
 __host__ __device__ inline size_t packed_offset(int row, int k, int rows, int kp) {
   const int b = k >> 6;
   const int rb = b == (kp >> 6) ? 32 : 64;
@@ -194,14 +194,15 @@ int f64_launch(const F64Problem* d_probs, const void* d_sched, int launch, hipSt
 // Launchers used by the orchestration (return 0 on success).
 // fold_q != 0: the residues of A plane l are (q_l r) mod p_l (symmetric) instead of r, with q_l the
 // CRT inverse of modulus l for the problem's N; the abs plane and B are unchanged.
-// fold_q: A residues carry the CRT inverses (production); packed: residue planes in the packed layout
+// fold_q: A residues carry the CRT inverses (production); packed_kp: the residue planes of problems
+// with Kp <= packed_kp are in the packed layout, the others row-major (0: every problem row-major)
 // max_moduli: the largest num_moduli among the num problems (selects the digit width)
 // yd (or nullptr): descriptors parallel to d whose nf summaries prep writes
 // order (or nullptr: 0 .. num - 1): the problems in the order their workgroups are dispatched
 // pofs (with order, or nullptr): a compact grid of total_blocks workgroups, problem order[i] owning
 // blocks pofs[i] .. pofs[i + 1] - 1 (ceil(m / 32) A-row blocks, then ceil(n / 8) B-column blocks;
 // none for problems prep skips)
-int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t s, int fold_q, int packed,
+int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t s, int fold_q, int packed_kp,
                 int max_moduli, const YDesc* yd = nullptr, const int* order = nullptr, const int* pofs = nullptr,
                 long long total_blocks = 0);
 // yd == nullptr: read the int32 planes of oz2_problem::C32 (kernel-level API); else the digits.

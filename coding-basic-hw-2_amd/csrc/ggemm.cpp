@@ -240,9 +240,12 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
   // Packed residue planes make every 64-byte k-stage of a tile's rows contiguous, which the INT8
   // GEMM's operand stream prefers at moderate k (measured: 1024^3 products 14 % faster together
   // with the blocked digits); at k = 16384 the row-major planes stream better (5 % slower packed).
+  // The choice is per problem (Kp <= packed_kp), so the long-k problems of a ragged group do not
+  // put its short ones on row-major planes.
   int max_kp = 0;
   for (int j = 0; j < c.ne; ++j) max_kp = std::max(max_kp, kp_of(probs[emu_idx[j]].k));
-  c.packed = !h->digits_colmajor && max_kp <= h->packed_max_kp;
+  c.packed_kp = h->digits_colmajor ? 0 : h->packed_max_kp;
+  c.packed = max_kp <= c.packed_kp;
   c.dot_form = h->dot_form;
   if (c.blocked) SY = SYb;
   uint8_t* ybase = reinterpret_cast<uint8_t*>(h->C32);
@@ -307,7 +310,7 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
         hepi[q] = I8Epi{0u, 1u, 0u, 0u};
       }
       if (c.blocked) hepi[q].mode |= kEpiBlocked;
-      if (c.packed) hepi[q].mode |= kEpiPacked;
+      if ((int)kp <= c.packed_kp) hepi[q].mode |= kEpiPacked;
     }
     const size_t plane = c.blocked ? blocked_plane_entries(p.m, p.n) : (size_t)p.m * p.n;
     oy += align_up(plane, kBufAlign);
@@ -385,7 +388,7 @@ int enqueue_grouped(const GroupedCall& c, const char* db, hipStream_t s, int rep
   if (c.ne > 0) {
     const bool shared = c.nprep > 0;   // operand reuse: prep once per unique operand
     if (prep_launch(shared ? reinterpret_cast<const oz2_problem*>(db + c.L.off_prep) : doz, shared ? c.nprep : c.ne,
-                    shared ? c.pmax_m : c.max_m, shared ? c.pmax_n : c.max_n, s, 1, c.packed, c.nmax,
+                    shared ? c.pmax_m : c.max_m, shared ? c.pmax_n : c.max_n, s, 1, c.packed_kp, c.nmax,
                     shared ? nullptr : dyd, reinterpret_cast<const int*>(db + c.L.off_po),
                     reinterpret_cast<const int*>(db + c.L.off_po) + (shared ? c.nprep : c.ne), c.prep_blocks))
       return GGEMM_ERR_NUMERICS;
@@ -559,7 +562,7 @@ int path_emu_loop(ggemm_handle_t h, bool batched, const ggemm_problem_t* probs, 
   const int i8k = h->i8_persistent ? kI8Persistent : kI8General;
   for (int j = 0; j < c.ne && !r; ++j) {
     const int planes = hoz[j].num_moduli + OZ2_EXTRA_PLANES;
-    if (prep_launch(doz + j, 1, hoz[j].m, hoz[j].n, h->stream, 1, c.packed, hoz[j].num_moduli, dyd + j)) {
+    if (prep_launch(doz + j, 1, hoz[j].m, hoz[j].n, h->stream, 1, c.packed_kp, hoz[j].num_moduli, dyd + j)) {
       r = GGEMM_ERR_NUMERICS;
       break;
     }

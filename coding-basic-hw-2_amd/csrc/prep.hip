@@ -618,7 +618,7 @@ template <bool kWide>
 __global__ void __launch_bounds__(kThreads, 4) prep_kernel(const oz2_problem* __restrict__ probs, int a_blocks,
                                                         const CrtTables* __restrict__ tab,
                                                         unsigned long long* __restrict__ cnt, int fold_q,
-                                                        int packed, const YDesc* __restrict__ yds,
+                                                        int packed_kp, const YDesc* __restrict__ yds,
                                                         const int* __restrict__ order, const int* __restrict__ pofs,
                                                         int nprob) {
   __shared__ PrepShared sm;
@@ -641,11 +641,12 @@ __global__ void __launch_bounds__(kThreads, 4) prep_kernel(const oz2_problem* __
   if (N < 1 || N > kMaxModuli || pr.alpha == 0.0) return;   // alpha == 0: A, B never referenced
   // folded A residues use the weights q 2^(8 i) mod p, so that sum b_i [q 2^(8 i)] = q x (mod p)
   const bool fold = fold_q && blk < a_blocks;
+  const bool packed = pr.kp <= packed_kp;   // packed_kp = 0: row-major (every Kp >= 32)
   if (blk < a_blocks) {
     if (blk * kARows >= pr.m) return;
-    prep_rows<kWide>(pr, tab, blk, blockIdx.z, gridDim.z, sm, cnt, fold ? N : 0, packed != 0, nfo);
+    prep_rows<kWide>(pr, tab, blk, blockIdx.z, gridDim.z, sm, cnt, fold ? N : 0, packed, nfo);
   } else {
-    prep_cols<kWide>(pr, tab, blk - a_blocks, blockIdx.z, gridDim.z, sm, cnt, packed != 0, nfo);
+    prep_cols<kWide>(pr, tab, blk - a_blocks, blockIdx.z, gridDim.z, sm, cnt, packed, nfo);
   }
 }
 
@@ -653,7 +654,7 @@ int g_force_split = 0;
 
 }  // namespace
 
-int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t s, int fold_q, int packed,
+int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t s, int fold_q, int packed_kp,
                 int max_moduli, const YDesc* yd, const int* order, const int* pofs, long long total_blocks) {
   if (num <= 0) return 0;
   if (num > 65535 || max_m < 0 || max_n < 0 || max_moduli < 1 || max_moduli > kMaxModuli) return 1;
@@ -673,11 +674,11 @@ int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t
   if (!ht) return 2;
   const dim3 g3(grid.x, grid.y, S);
   if (ht->T[max_moduli] < 0x1.8p62)
-    hipLaunchKernelGGL(prep_kernel<false>, g3, dim3(kThreads), 0, s, d, a_blocks, c->tab, c->counters, fold_q, packed,
-                       yd, order, pofs, num);
+    hipLaunchKernelGGL(prep_kernel<false>, g3, dim3(kThreads), 0, s, d, a_blocks, c->tab, c->counters, fold_q,
+                       packed_kp, yd, order, pofs, num);
   else
-    hipLaunchKernelGGL(prep_kernel<true>, g3, dim3(kThreads), 0, s, d, a_blocks, c->tab, c->counters, fold_q, packed,
-                       yd, order, pofs, num);
+    hipLaunchKernelGGL(prep_kernel<true>, g3, dim3(kThreads), 0, s, d, a_blocks, c->tab, c->counters, fold_q,
+                       packed_kp, yd, order, pofs, num);
   return hipGetLastError() == hipSuccess ? 0 : 3;
 }
 

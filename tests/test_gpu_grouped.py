@@ -320,16 +320,19 @@ def test_default_kernel_choice():
 
 
 def test_default_layout_long_k_matches_oracle():
-    """The production layout of every call whose largest Kp exceeds 4096 -- row-major residue
-    planes, 16 x 16 blocked digits -- bitwise against the oracle in COUNT mode (uncertified entries
-    keep their emulated values), on the default handle (general INT8 kernel for this small group)
-    and with the 256 x 256 kernel forced; mixed N (15 at k <= 5000, 16 at k = 16384); odd row
-    counts, a single-row problem, ragged tile edges and final half k-stages (Kp % 64 = 32)."""
-    case = Case([(256, 256, 4160)] * 3 + [(128, 96, 16384), (257, 129, 4097), (3, 1, 4200), (255, 63, 5000)],
+    """The production layout of a call whose largest Kp exceeds 4096 -- row-major residue planes
+    for the problems with Kp > 4096, packed planes for the others (Kp = 1024, and 4096 exactly and
+    by rounding k = 4065 up), 16 x 16 blocked digits -- bitwise against the oracle in COUNT mode
+    (uncertified entries keep their emulated values), on the default handle (general INT8 kernel
+    for this small group) and with the 256 x 256 kernel forced; mixed N (15 at k <= 5000, 16 at
+    k = 16384); odd row counts, a single-row problem, ragged tile edges and final half k-stages
+    (Kp % 64 = 32)."""
+    case = Case([(256, 256, 4160)] * 3 + [(128, 96, 16384), (257, 129, 4097), (3, 1, 4200), (255, 63, 5000),
+                                          (200, 150, 1000), (64, 300, 4096), (33, 17, 4065)],
                 20261230, phi=1.0, beta=0.5)
     cfg = G.Config(0, 1e-15, 0, G.REPAIR_COUNT)
     rc, plan = oracle_plan(case, cfg, G.PATH_EMU_GROUPED)
-    assert rc == 0 and [e.num_moduli for e in plan] == [15, 15, 15, 16, 15, 15, 15]
+    assert rc == 0 and [e.num_moduli for e in plan] == [15, 15, 15, 16, 15, 15, 15, 15, 15, 15]
     want = [h.emulate(O.REPAIR_COUNT, e.num_moduli) for h, e in zip(case.hp, plan)]
     for kernel, name in ((None, "i8_grouped_kernel"), ("large", "i8_large_kernel")):
         say(f"long-k default layout, kernel {name}")
