@@ -278,14 +278,35 @@ __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ t
   double mx = 0.0, ss = 0.0;
   if (valid) {
     int k = c;
-    for (; k + 8 * 15 < K; k += 8 * 16) {   // 16 loads in flight, then the ordered chain
-      double a[16];
+    // groups of 16 k per chain, software-pipelined: the next group's loads are issued before this
+    // group's chain, so 16 to 32 loads stay in flight (a long-k block is one of few workgroups and
+    // streams megabytes); the load past the last group re-reads it (in bounds) so that the load
+    // count between two waits is the same on every path
+    auto ld16 = [&](double (&a)[16], int k0) {
 #pragma unroll
-      for (int t = 0; t < 16; ++t) a[t] = A[i + (size_t)(k + 8 * t) * lda];
+      for (int t = 0; t < 16; ++t) a[t] = A[i + (size_t)(k0 + 8 * t) * lda];
+    };
+    auto chain16 = [&](const double (&a)[16]) {
 #pragma unroll
       for (int t = 0; t < 16; ++t) {
         mx = fmax(mx, fabs(a[t]));
         ss = fma(a[t], a[t], ss);
+      }
+    };
+    if (k + 8 * 15 < K) {
+      double a[16], b[16];
+      ld16(a, k);
+      for (;;) {
+        bool more = k + 8 * 31 < K;
+        ld16(b, more ? k + 128 : k);
+        chain16(a);
+        k += 128;
+        if (!more) break;
+        more = k + 8 * 31 < K;
+        ld16(a, more ? k + 128 : k);
+        chain16(b);
+        k += 128;
+        if (!more) break;
       }
     }
     for (; k < K; k += 8) {
@@ -452,14 +473,32 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
     }
   } else {
     int k = lane;
-    for (; k + 32 * 7 < K; k += 32 * 8) {   // 8 loads in flight, then the ordered chain
-      double a[8];
+    // groups of 16 k per lane, software-pipelined as in the A-row pass (16 to 32 loads in flight)
+    auto ld16 = [&](double (&a)[16], int k0) {
 #pragma unroll
-      for (int t = 0; t < 8; ++t) a[t] = b[k + 32 * t];
+      for (int t = 0; t < 16; ++t) a[t] = b[k0 + 32 * t];
+    };
+    auto chain16 = [&](const double (&a)[16]) {
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
+      for (int t = 0; t < 16; ++t) {
         mx = fmax(mx, fabs(a[t]));
         ss = fma(a[t], a[t], ss);
+      }
+    };
+    if (k + 32 * 15 < K) {
+      double a[16], c[16];
+      ld16(a, k);
+      for (;;) {
+        bool more = k + 32 * 31 < K;
+        ld16(c, more ? k + 512 : k);
+        chain16(a);
+        k += 512;
+        if (!more) break;
+        more = k + 32 * 31 < K;
+        ld16(a, more ? k + 512 : k);
+        chain16(c);
+        k += 512;
+        if (!more) break;
       }
     }
     for (; k < K; k += 32) {
