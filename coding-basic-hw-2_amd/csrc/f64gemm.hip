@@ -132,12 +132,31 @@ __global__ void __launch_bounds__(kThreads, T == 64 ? 5 : 2) f64_grouped_kernel(
     }
   }
   // D block layout of v_mfma_f64_16x16x4f64: lane l, register r -> row 4 r + l / 16, column l % 16
-  // (four single-row groups; the INT8 / F32 16 x 16 instructions use four consecutive rows instead)
+  // (four single-row groups; the INT8 / F32 16 x 16 instructions use four consecutive rows instead).
+  // With beta != 0 the C0 values of a batch of blocks are all loaded before the batch's stores:
+  // entry by entry, each C0 load waited for its data before the store (the stores might alias
+  // the next loads), one memory round trip per entry.
   const size_t ldc = (size_t)P.ldc;
+  GLOBAL double* const Cg = (GLOBAL double*)P.C;
+  const bool rd = P.beta != 0.0;
+  constexpr int NBLK = FB * FB, BATCH = NBLK < 8 ? NBLK : 8;
 #pragma unroll
-  for (int i = 0; i < FB; ++i)
+  for (int b0 = 0; b0 < NBLK; b0 += BATCH) {
+    double c0[BATCH][4];
 #pragma unroll
-    for (int j = 0; j < FB; ++j) {
+    for (int q = 0; q < BATCH; ++q) {
+      const int i = (b0 + q) / FB, j = (b0 + q) % FB;
+      const int col = col0 + wn * (T / 2) + j * 16 + (lane & 15);
+      const int rbase = row0 + wm * (T / 2) + i * 16 + (lane >> 4);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = rbase + 4 * r;
+        c0[q][r] = (rd && col < P.n && row < P.m) ? Cg[(size_t)row + (size_t)col * ldc] : 0.0;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < BATCH; ++q) {
+      const int i = (b0 + q) / FB, j = (b0 + q) % FB;
       const int col = col0 + wn * (T / 2) + j * 16 + (lane & 15);
       const int rbase = row0 + wm * (T / 2) + i * 16 + (lane >> 4);
       if (col >= P.n) continue;
@@ -145,11 +164,11 @@ __global__ void __launch_bounds__(kThreads, T == 64 ? 5 : 2) f64_grouped_kernel(
       for (int r = 0; r < 4; ++r) {
         const int row = rbase + 4 * r;
         if (row >= P.m) continue;
-        GLOBAL double* cp = (GLOBAL double*)P.C + (size_t)row + (size_t)col * ldc;
         const double ab = compute ? P.alpha * acc[i][j][r] : 0.0;
-        *cp = (P.beta == 0.0) ? ab : (compute ? ab + P.beta * *cp : P.beta * *cp);
+        Cg[(size_t)row + (size_t)col * ldc] = !rd ? ab : (compute ? ab + P.beta * c0[q][r] : P.beta * c0[q][r]);
       }
     }
+  }
 }
 
 }  // namespace
