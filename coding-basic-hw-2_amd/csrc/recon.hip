@@ -513,48 +513,19 @@ static_assert(4 * kDK * kRT <= kUnion && 2 * 1024 <= kUnion, "dot-pass LDS union
 __device__ __forceinline__ void lds_sync() { __syncthreads(); }
 
 // The fp64 dot product of a safety-fallback entry (row i of A or column j of B holds a NaN or an
-// Inf) without its chain.  The chain s = fma(a_k, b_k, s) from s = 0 ends non-finite: a product
-// with an infinite factor is +-Inf, or NaN when the other factor is 0 or NaN; an infinite s stays
-// so under finite addends and turns NaN under the opposite infinity; NaN stays NaN.  Its value is
-// therefore NaN if a NaN factor occurs, if an infinity meets a zero or if infinite products of both
-// signs occur, and otherwise the one signed infinity -- provided no finite partial sum overflows
-// before the first infinite product.  Those sums stay below k 2^(eA + 1) 2^(eB + 1) (1 + u)^k <
-// 2^(eA + eB + 3 + ceil(log2 k)) (eA, eB: ilogb of the largest finite magnitudes of the row and
-// the column), so eA + eB + 3 + ceil(log2 k) <= 1023 rules overflow out.  Returns false (the entry
-// takes its chain) outside that bound or when the row or column has more infinities than its
-// summary lists.  The result equals the chain's bit for bit except for a NaN's payload.
-// hr / eA: the row's summary words 0 and 1 (rnf) or 0 and its exponent from sigma; likewise hc / eB.
-__device__ __forceinline__ bool nf_dot(const oz2_problem& pr, const GLOBAL int32_t* R, const GLOBAL int32_t* Cl,
-                                       int i, int j, int hr, int eA, int hc, int eB, double& d) {
-  if ((hr | hc) & 1) {
-    d = __builtin_nan("");
-    return true;
-  }
-  const int K = pr.k;
-  const int lk = K > 1 ? 32 - __clz(K - 1) : 0;
-  if (((hr | hc) & 2) || eA + eB + 3 + lk > 1023) return false;
-  bool nan = false, pos = false, neg = false;
-  const int nr = (hr >> 8) & 0xff, nc = (hc >> 8) & 0xff;
-  const GLOBAL double* b = gp(pr.B) + (size_t)j * pr.ldb;
-  for (int s = 0; s < nr; ++s) {   // row infinities: a_k = +-Inf against b_k
-    const int w = R[2 + s];
-    const double x = b[w & 0x7fffffff];
-    if (x == 0.0 || isnan(x)) nan = true;
-    else if ((w < 0) != (x < 0.0)) neg = true;
-    else pos = true;
-  }
-  const GLOBAL double* a = gp(pr.A) + i;
-  for (int s = 0; s < nc; ++s) {   // column infinities: b_k = +-Inf against a_k
-    const int w = Cl[2 + s];
-    const double x = a[(size_t)(w & 0x7fffffff) * pr.lda];
-    if (x == 0.0 || isnan(x)) nan = true;
-    else if ((w < 0) != (x < 0.0)) neg = true;
-    else pos = true;
-  }
-  if (!(nan || pos || neg)) return false;   // no infinity listed (not a safety entry)
-  d = (nan || (pos && neg)) ? __builtin_nan("") : (pos ? __builtin_inf() : -__builtin_inf());
-  return true;
-}
+// Inf) without its chain (the summary rule, applied in dots_kernel).  The chain s = fma(a_k, b_k, s)
+// from s = 0 ends non-finite: a product with an infinite factor is +-Inf, or NaN when the other
+// factor is 0 or NaN; an infinite s stays so under finite addends and turns NaN under the opposite
+// infinity; NaN stays NaN.  Its value is therefore NaN if a NaN factor occurs, if an infinity meets
+// a zero or if infinite products of both signs occur, and otherwise the one signed infinity --
+// provided no finite partial sum overflows before the first infinite product.  Those sums stay
+// below k 2^(eA + 1) 2^(eB + 1) (1 + u)^k < 2^(eA + eB + 3 + ceil(log2 k)) (eA, eB: ilogb of the
+// largest finite magnitudes of the row and the column), so eA + eB + 3 + ceil(log2 k) <= 1023 rules
+// overflow out.  Outside that bound, when the row or column has more infinities than its summary
+// lists, or when none is listed, the entry takes its chain.  The result equals the chain's bit for
+// bit except for a NaN's payload.  Row summary words 0 and 1 (or 0 and the exponent from sigma for
+// a finite row) give hr / eA, likewise hc / eB for the column; a row infinity at k = w pairs with
+// B(w, j), a column infinity with A(i, w).
 
 __device__ __forceinline__ unsigned long long uniform_u64(unsigned long long v) {
   const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
@@ -853,45 +824,146 @@ __global__ void __launch_bounds__(kThreads, 5) dots_kernel(const oz2_problem* __
   if (total == 0) return;   // workgroup-uniform
   const GLOBAL int32_t* const nf = gp(yds[pi].nf);
   if (nf) {
-    // safety-fallback entries from the summaries: thread t takes row il = t % 64 of the tile in
-    // columns jl = 16 (t / 64) .. + 15 (the column's summary is wave-uniform, C stores contiguous);
-    // decided entries are stored and their flags cleared
-    const int il = t & 63, i = r0 + il;
-    if (i < m) {
-      const GLOBAL int32_t* rs = gp(pr.row_shift);
-      const GLOBAL int32_t* cs = gp(pr.col_shift);
-      const int rsh = rs[i], sg = rs[m + i];
-      const bool rnf = rsh == OZ2_SHIFT_NONFINITE;
-      const GLOBAL int32_t* R = nf + (size_t)kNfWords * i;
-      int hr = 0, eA = sg == OZ2_SHIFT_ZERO ? kNfNoFinite : 6 - sg;
-      if (rnf) {
-        hr = R[0];
-        eA = R[1];
-      }
-      for (int q = 0; q < 16; ++q) {
-        const int jl = 16 * (t >> 6) + q, j = c0 + jl;
-        const int wi = 4 * (4 * (jl >> 4) + (il >> 4)) + (il & 3);
-        const uint64_t bit = 1ull << (16 * ((il & 15) >> 2) + (jl & 15));
-        if (j >= n || !(fl[wi] & bit)) continue;
-        const int csh = cs[j];
-        const bool cnf = csh == OZ2_SHIFT_NONFINITE;
-        if (!rnf && !cnf) continue;   // a repair
-        const GLOBAL int32_t* Cl = nf + (size_t)kNfWords * ((size_t)m + j);
-        int hc = 0, eB;
-        if (cnf) {
+    // safety-fallback entries from the summaries (nf_dot's rule): thread t takes row il = t % 64 of
+    // the tile in columns jl = 16 (t / 64) .. + 15; decided entries are stored and their flags
+    // cleared.  The tile's 64 column summaries are staged in LDS once, a thread keeps its row's
+    // summary and infinity list in registers, and the partner loads of its entries are issued
+    // together (8 at a time), one listed infinity after the other (entry after entry they were
+    // chains of dependent loads, flag -> column summary -> list -> partner).
+    const GLOBAL int32_t* rs = gp(pr.row_shift);
+    const GLOBAL int32_t* cs = gp(pr.col_shift);
+    int* const cinf = reinterpret_cast<int*>(buf);   // [64][4]: non-finite column, h word, exponent, listed
+    int* const clst = cinf + 4 * kRT;                // [64][kNfCap]: the column's infinities
+    if (t < kRT) {
+      const int j = c0 + t;
+      int cnf = 0, hc = 0, eB = kNfNoFinite, nc = 0;
+      if (j < n) {
+        if (cs[j] == OZ2_SHIFT_NONFINITE) {
+          const GLOBAL int32_t* Cl = nf + (size_t)kNfWords * ((size_t)m + j);
+          cnf = 1;
           hc = Cl[0];
           eB = Cl[1];
+          nc = min((hc >> 8) & 0xff, kNfCap);
+#pragma unroll
+          for (int s = 0; s < kNfCap; ++s)
+            if (s < nc) clst[t * kNfCap + s] = Cl[2 + s];
         } else {
           const int tau = cs[n + j];
           eB = tau == OZ2_SHIFT_ZERO ? kNfNoFinite : 6 - tau;
         }
-        double d;
-        if (nf_dot(pr, R, Cl, i, j, hr, eA, hc, eB, d)) {
-          GLOBAL double* cp = gpw(pr.C) + i + (size_t)j * pr.ldc;
-          *cp = from_dot(alpha, beta, d, beta != 0.0 ? *cp : 0.0);
-          atomicAnd(reinterpret_cast<unsigned long long*>(&fl[wi]), ~(unsigned long long)bit);
+      }
+      cinf[4 * t] = cnf;
+      cinf[4 * t + 1] = hc;
+      cinf[4 * t + 2] = eB;
+      cinf[4 * t + 3] = nc;
+    }
+    lds_sync();
+    const int il = t & 63, i = r0 + il, jb = 16 * (t >> 6);
+    const int K = pr.k;
+    const int lk = K > 1 ? 32 - __clz(K - 1) : 0;
+    unsigned cand = 0u, nanm = 0u, posm = 0u, negm = 0u;   // bit q: column jb + q
+    int hr = 0, eA = kNfNoFinite, nr = 0;
+    int rl[kNfCap] = {};
+    if (i < m) {
+      const int rsh = rs[i], sg = rs[m + i];
+      const bool rnf = rsh == OZ2_SHIFT_NONFINITE;
+      const GLOBAL int32_t* R = nf + (size_t)kNfWords * i;
+      eA = sg == OZ2_SHIFT_ZERO ? kNfNoFinite : 6 - sg;
+      if (rnf) {
+        hr = R[0];
+        eA = R[1];
+      }
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int jl = jb + q;
+        const int wi = 4 * (4 * (jl >> 4) + (il >> 4)) + (il & 3);
+        const uint64_t bit = 1ull << (16 * ((il & 15) >> 2) + (jl & 15));
+        if (c0 + jl >= n || !(fl[wi] & bit)) continue;
+        const int cnf = cinf[4 * jl], hc = cinf[4 * jl + 1], eB = cinf[4 * jl + 2];
+        if (!rnf && !cnf) continue;   // a repair
+        if ((hr | hc) & 1) {          // a NaN factor: NaN
+          nanm |= 1u << q;
+          continue;
+        }
+        if (((hr | hc) & 2) || eA + eB + 3 + lk > 1023) continue;   // its chain decides
+        cand |= 1u << q;
+      }
+      nr = cand ? min((hr >> 8) & 0xff, kNfCap) : 0;
+#pragma unroll
+      for (int s = 0; s < kNfCap; ++s) rl[s] = s < nr ? R[2 + s] : 0;
+    }
+    // a partner x of an infinity of sign ng: NaN for 0 or NaN, else the product's sign
+    auto cls = [&](double x, bool ng, int q) {   // selects, not branches (no mask array in scratch)
+      const unsigned b = 1u << q;
+      const bool z = x == 0.0 || isnan(x), o = ng != (x < 0.0);
+      nanm |= z ? b : 0u;
+      negm |= (!z && o) ? b : 0u;
+      posm |= (!z && !o) ? b : 0u;
+    };
+    // row infinities: B(w, j) of every candidate entry, one listed infinity at a time
+    int nrm = nr;
+#pragma unroll
+    for (int o = 32; o; o >>= 1) nrm = max(nrm, __shfl_xor(nrm, o));
+    const GLOBAL double* const Bg = gp(pr.B);
+    const GLOBAL double* const Ag = gp(pr.A);
+    const size_t ldb = (size_t)pr.ldb, lda = (size_t)pr.lda;
+#pragma unroll
+    for (int s = 0; s < kNfCap; ++s) {
+      if (s < nrm) {   // wave-uniform
+        const bool act = s < nr;
+        const int w = rl[s];
+#pragma unroll
+        for (int h = 0; h < 16; h += 8) {   // 8 loads in flight at a time (the kernel's register budget)
+          double x[8];
+#pragma unroll
+          for (int q = 0; q < 8; ++q)
+            x[q] = (act && ((cand >> (h + q)) & 1u)) ? Bg[(size_t)(w & 0x7fffffff) + (size_t)(c0 + jb + h + q) * ldb] : 0.0;
+#pragma unroll
+          for (int q = 0; q < 8; ++q)
+            if (act && ((cand >> (h + q)) & 1u)) cls(x[q], w < 0, h + q);
         }
       }
+    }
+    // column infinities: A(i, w); a wave's 16 columns are the same in every lane
+    int ncm = 0;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) ncm = max(ncm, cinf[4 * (jb + q) + 3]);
+    for (int s = 0; s < ncm; ++s) {   // wave-uniform trip count
+#pragma unroll
+      for (int h = 0; h < 16; h += 8) {
+        double x[8];
+        int wv[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const bool act = ((cand >> (h + q)) & 1u) && s < cinf[4 * (jb + h + q) + 3];
+          wv[q] = act ? clst[(jb + h + q) * kNfCap + s] : 0;
+          x[q] = act ? Ag[(size_t)i + (size_t)(wv[q] & 0x7fffffff) * lda] : 0.0;
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+          if (((cand >> (h + q)) & 1u) && s < cinf[4 * (jb + h + q) + 3]) cls(x[q], wv[q] < 0, h + q);
+      }
+    }
+    // decided entries: NaN if a NaN factor, a zero / NaN partner or products of both signs
+    // occur, else the one signed infinity; a candidate with no partner keeps its chain
+    const unsigned dec = nanm | posm | negm;
+#pragma unroll
+    for (int h = 0; h < 16; h += 8) {
+      double cv[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        cv[q] = (beta != 0.0 && ((dec >> (h + q)) & 1u)) ? gp(pr.C)[(size_t)i + (size_t)(c0 + jb + h + q) * pr.ldc] : 0.0;
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        if ((dec >> (h + q)) & 1u) {
+          const int jl = jb + h + q;
+          const bool isnan_ = ((nanm >> (h + q)) & 1u) || (((posm & negm) >> (h + q)) & 1u);
+          const double d = isnan_ ? __builtin_nan("") : (((posm >> (h + q)) & 1u) ? __builtin_inf() : -__builtin_inf());
+          gpw(pr.C)[(size_t)i + (size_t)(c0 + jl) * pr.ldc] = from_dot(alpha, beta, d, cv[q]);
+          const int wi = 4 * (4 * (jl >> 4) + (il >> 4)) + (il & 3);
+          const uint64_t bit = 1ull << (16 * ((il & 15) >> 2) + (jl & 15));
+          atomicAnd(reinterpret_cast<unsigned long long*>(&fl[wi]), ~(unsigned long long)bit);
+        }
     }
     lds_sync();
     count_flags(fl, &cnt[0]);
