@@ -228,27 +228,6 @@ struct PrepShared {
   unsigned long long nfmx[kARows];
 };
 
-// One row's / column's values a[e] at k = kb + ks e (zeros past K) into its summary: infinities
-// listed at nfw + 2 .. (slots from an LDS counter, any order), NaN and the largest finite magnitude
-// into LDS.  The summary state stays in LDS, so none of it is live across the residue loops.
-__device__ __forceinline__ void nf_scan(const double (&a)[4], int kb, int ks, GLOBAL int32_t* nfw, int* ncnt, int* nnan,
-                                        unsigned long long* nmx) {
-  double mt = 0.0;
-  bool nn = false;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    if (isnan(a[e])) {
-      nn = true;
-    } else if (isinf(a[e])) {
-      const int x = atomicAdd(ncnt, 1);
-      if (x < kNfCap) nfw[2 + x] = (kb + ks * e) | (a[e] < 0.0 ? (int)0x80000000u : 0);
-    } else {
-      mt = fmax(mt, fabs(a[e]));
-    }
-  }
-  if (nn) *nnan = 1;
-  if (mt > 0.0) atomicMax(nmx, (unsigned long long)__double_as_longlong(mt));
-}
 // The summary's words 0 and 1 from the LDS state.
 __device__ __forceinline__ void nf_header(GLOBAL int32_t* nfw, int ni, int nan, unsigned long long mx) {
   nfw[0] = (nan ? 1 : 0) | (ni > kNfCap ? 2 : 0) | (min(ni, kNfCap) << 8);
@@ -260,10 +239,17 @@ template <bool kWide>
 __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ tab, int blk, int split,
                           int nsplit, PrepShared& sm, unsigned long long* cnt, int widx, bool packed, int32_t* nfo) {
   const int tid = threadIdx.x;
-  if (tid < kARows) {   // ordered before their atomics by the barriers of pass 1
-    sm.nfcnt[tid] = 0;
-    sm.nfnan[tid] = 0;
-    sm.nfmx[tid] = 0ull;
+  // split 0, when the call asks for summaries: pass 1, which reads every value of the block's rows,
+  // also collects each row's non-finite summary state (NaN seen, largest finite magnitude,
+  // infinity positions); it is written for the rows whose shift turns out non-finite
+  const bool trk = nfo && split == 0;   // block-uniform
+  if (trk) {
+    if (tid < kARows) {
+      sm.nfcnt[tid] = 0;
+      sm.nfnan[tid] = 0;
+      sm.nfmx[tid] = 0ull;
+    }
+    __syncthreads();
   }
   const int N = pr.num_moduli, K = pr.k, Kp = pr.kp, m = pr.m;
   const int row0 = blk * kARows;
@@ -274,8 +260,24 @@ __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ t
   const size_t lda = (size_t)pr.lda;
   const double T = tab->T[N];
 
-  // ---- pass 1: row max and sum of squares, chain c = k mod 8 ascending
+  // ---- pass 1: row max and sum of squares, chain c = k mod 8 ascending.  With trk, mx is the
+  // largest FINITE magnitude and every infinity is listed instead; the row max is then infinite
+  // exactly when the row's infinity count is nonzero, so the shift is the same
   double mx = 0.0, ss = 0.0;
+  auto step = [&](double a, int k) {
+    ss = fma(a, a, ss);
+    if (!trk) {
+      mx = fmax(mx, fabs(a));
+      return;
+    }
+    const double aa = fabs(a);
+    const bool inf = aa == __builtin_inf();
+    mx = fmax(mx, inf ? 0.0 : aa);
+    if (inf) {   // rare: the summary's address is formed here, not kept live through the pass
+      const int x = atomicAdd(&sm.nfcnt[r], 1);
+      if (x < kNfCap) ((GLOBAL int32_t*)nfo)[(size_t)kNfWords * i + 2 + x] = k | (a < 0.0 ? (int)0x80000000u : 0);
+    }
+  };
   if (valid) {
     int k = c;
     // groups of 16 k per chain, software-pipelined: the next group's loads are issued before this
@@ -286,12 +288,9 @@ __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ t
 #pragma unroll
       for (int t = 0; t < 16; ++t) a[t] = A[i + (size_t)(k0 + 8 * t) * lda];
     };
-    auto chain16 = [&](const double (&a)[16]) {
+    auto chain16 = [&](const double (&a)[16], int k0) {
 #pragma unroll
-      for (int t = 0; t < 16; ++t) {
-        mx = fmax(mx, fabs(a[t]));
-        ss = fma(a[t], a[t], ss);
-      }
+      for (int t = 0; t < 16; ++t) step(a[t], k0 + 8 * t);
     };
     if (k + 8 * 15 < K) {
       double a[16], b[16];
@@ -299,32 +298,34 @@ __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ t
       for (;;) {
         bool more = k + 8 * 31 < K;
         ld16(b, more ? k + 128 : k);
-        chain16(a);
+        chain16(a, k);
         k += 128;
         if (!more) break;
         more = k + 8 * 31 < K;
         ld16(a, more ? k + 128 : k);
-        chain16(b);
+        chain16(b, k);
         k += 128;
         if (!more) break;
       }
     }
-    for (; k < K; k += 8) {
-      const double a = A[i + (size_t)k * lda];
-      mx = fmax(mx, fabs(a));
-      ss = fma(a, a, ss);
-    }
+    for (; k < K; k += 8) step(A[i + (size_t)k * lda], k);
+    if (trk && isnan(ss)) sm.nfnan[r] = 1;   // a sum of squares turns NaN only through a NaN
   }
   sm.red0[c][r] = mx;
   __syncthreads();
   if (c == 0) {
     double M = 0.0;
     for (int q = 0; q < kChains; ++q) M = fmax(M, sm.red0[q][r]);
+    if (trk) {   // M is the largest finite magnitude: the summary's, and infinite row max if any Inf
+      sm.nfmx[r] = (unsigned long long)__double_as_longlong(M);
+      if (sm.nfcnt[r] > 0) M = __builtin_inf();
+    }
     sm.rowmax[r] = M;
   }
   __syncthreads();
   const double rowmax = sm.rowmax[r];
-  const bool resc = valid && needs_rescale(rowmax);
+  // (an infinite row max already makes the shift non-finite: no rescaled second read of the row)
+  const bool resc = valid && isfinite(rowmax) && needs_rescale(rowmax);
   if (resc) {   // rare: exact power-of-two prescaling so the squares cannot overflow / underflow
     const int e = -ilogb(rowmax);
     ss = 0.0;
@@ -359,9 +360,7 @@ __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ t
   const bool nf_r = sh_r == OZ2_SHIFT_NONFINITE;
   const bool rvalid = row0 + rr < m;
   double da2 = 0.0, na2 = 0.0;
-  // split 0, rows holding a NaN / Inf, when the call asks for summaries: whether a NaN occurs, the
-  // largest finite magnitude and the infinities' positions, from the values this pass loads anyway
-  const bool nfr = nfo && nf_c && valid && split == 0;
+  const bool nfr = trk && nf_c && valid;   // the row's summary is written (state from pass 1)
   const int ntile = (Kp + kATile - 1) / kATile;
   const int per = (ntile + nsplit - 1) / nsplit;
   const int w0 = min(ntile, split * per), w1 = min(ntile, w0 + per);   // tiles written here
@@ -370,17 +369,9 @@ __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ t
     const int k0 = t * kATile;
     double av[kATile / kChains];
 #pragma unroll
-    for (int jj = 0; jj < kATile / kChains; ++jj) {
+    for (int jj = 0; jj < kATile / kChains; ++jj) {   // non-finite rows: zero residues, nothing to read
       const int k = k0 + c + kChains * jj;
-      av[jj] = (valid && k < K) ? A[i + (size_t)k * lda] : 0.0;
-    }
-    if (nfr) {
-      GLOBAL int32_t* const nfw = (GLOBAL int32_t*)nfo + (size_t)kNfWords * i;
-#pragma unroll
-      for (int g = 0; g < kATile / kChains / 4; ++g) {
-        const double a[4] = {av[4 * g], av[4 * g + 1], av[4 * g + 2], av[4 * g + 3]};
-        nf_scan(a, k0 + c + kChains * 4 * g, kChains, nfw, &sm.nfcnt[r], &sm.nfnan[r], &sm.nfmx[r]);
-      }
+      av[jj] = (valid && !nf_c && k < K) ? A[i + (size_t)k * lda] : 0.0;
     }
     if (!nf_c && split == 0) {
       double xs[kATile / kChains];
@@ -455,6 +446,12 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   const GLOBAL double* __restrict__ b = (const GLOBAL double*)pr.B + (size_t)j * pr.ldb;
   const double T = tab->T[N];
+  // split 0 with summaries: pass 1 collects the column's summary state, as for the A rows (mx the
+  // largest finite magnitude, the infinities listed)
+  const bool trk = nfo && split == 0;   // column-uniform
+  // (the summary's address is formed where it is used: a pointer live through the passes would
+  // take the kernel past its register budget)
+  auto nfw = [&]() { return (GLOBAL int32_t*)nfo + (size_t)kNfWords * ((size_t)pr.m + j); };
 
   // K <= 32 kBReg: the column is read once; lane l keeps k = l + 32 t in registers (its norm chain,
   // zeros past K change neither the max nor the sums) and gets the residue pass's 4 consecutive k
@@ -463,6 +460,20 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
   const bool single = !kWide && K <= 32 * kBReg;
   double v[kBReg];
   double mx = 0.0, ss = 0.0;
+  auto step = [&](double a, int k) {   // as for the A rows
+    ss = fma(a, a, ss);
+    if (!trk) {
+      mx = fmax(mx, fabs(a));
+      return;
+    }
+    const double aa = fabs(a);
+    const bool inf = aa == __builtin_inf();
+    mx = fmax(mx, inf ? 0.0 : aa);
+    if (inf) {
+      const int x = atomicAdd(&sm.nfcnt[w], 1);
+      if (x < kNfCap) nfw()[2 + x] = k | (a < 0.0 ? (int)0x80000000u : 0);
+    }
+  };
   if (single) {
 #pragma unroll
     for (int t = 0; t < kBReg; ++t) v[t] = lane + 32 * t < K ? b[lane + 32 * t] : 0.0;
@@ -471,6 +482,22 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
       mx = fmax(mx, fabs(v[t]));
       ss = fma(v[t], v[t], ss);
     }
+    // the values are still in registers: the summary state is collected only when the column
+    // turns out non-finite (any lane), from them
+    if (trk && __any(!isfinite(mx) || isnan(ss))) {
+      double mf = 0.0;
+#pragma unroll
+      for (int t = 0; t < kBReg; ++t) {
+        const double aa = fabs(v[t]);
+        const bool inf = aa == __builtin_inf();
+        mf = fmax(mf, inf ? 0.0 : aa);
+        if (inf) {
+          const int x = atomicAdd(&sm.nfcnt[w], 1);
+          if (x < kNfCap) nfw()[2 + x] = (lane + 32 * t) | (v[t] < 0.0 ? (int)0x80000000u : 0);
+        }
+      }
+      mx = mf;   // with trk, mx is the largest finite magnitude (the infinities are counted)
+    }
   } else {
     int k = lane;
     // groups of 16 k per lane, software-pipelined as in the A-row pass (16 to 32 loads in flight)
@@ -478,12 +505,9 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
 #pragma unroll
       for (int t = 0; t < 16; ++t) a[t] = b[k0 + 32 * t];
     };
-    auto chain16 = [&](const double (&a)[16]) {
+    auto chain16 = [&](const double (&a)[16], int k0) {
 #pragma unroll
-      for (int t = 0; t < 16; ++t) {
-        mx = fmax(mx, fabs(a[t]));
-        ss = fma(a[t], a[t], ss);
-      }
+      for (int t = 0; t < 16; ++t) step(a[t], k0 + 32 * t);
     };
     if (k + 32 * 15 < K) {
       double a[16], c[16];
@@ -491,25 +515,30 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
       for (;;) {
         bool more = k + 32 * 31 < K;
         ld16(c, more ? k + 512 : k);
-        chain16(a);
+        chain16(a, k);
         k += 512;
         if (!more) break;
         more = k + 32 * 31 < K;
         ld16(a, more ? k + 512 : k);
-        chain16(c);
+        chain16(c, k);
         k += 512;
         if (!more) break;
       }
     }
-    for (; k < K; k += 32) {
-      const double a = b[k];
-      mx = fmax(mx, fabs(a));
-      ss = fma(a, a, ss);
-    }
+    for (; k < K; k += 32) step(b[k], k);
   }
+  if (trk && isnan(ss)) sm.nfnan[w] = 1;   // a sum of squares turns NaN only through a NaN
 #pragma unroll
   for (int o = 16; o; o >>= 1) mx = fmax(mx, __shfl_xor(mx, o, 32));
-  const bool resc = needs_rescale(mx);
+  if (trk) {   // every lane's counter update precedes the reads; mx is the largest finite magnitude
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane == 0) sm.nfmx[w] = (unsigned long long)__double_as_longlong(mx);
+    if (sm.nfcnt[w] > 0) mx = __builtin_inf();
+  }
+  // (an infinite column max already makes the shift non-finite: no rescaled second read)
+  const bool resc = isfinite(mx) && needs_rescale(mx);
   if (resc) {
     const int e = -ilogb(mx);
     ss = 0.0;
@@ -537,12 +566,7 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
   }
   const bool nf = sh == OZ2_SHIFT_NONFINITE;
 
-  // split 0, columns holding a NaN / Inf, when the call asks for summaries (column-uniform)
-  const bool nfc = nfo && nf && split == 0;
-  auto nfw = [&]() { return (GLOBAL int32_t*)nfo + (size_t)kNfWords * ((size_t)pr.m + j); };
-  auto nfscan = [&](const double (&a)[4], int kb, int ks) {
-    nf_scan(a, kb, ks, nfw(), &sm.nfcnt[w], &sm.nfnan[w], &sm.nfmx[w]);
-  };
+  const bool nfc = trk && nf;   // the column's summary is written (state from pass 1; column-uniform)
 
   double da2 = 0.0, na2 = 0.0;
   GLOBAL int8_t* const B8 = (GLOBAL int8_t*)pr.B8;
@@ -585,13 +609,6 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
     // lane l holds k = 128 ch + 32 jj + l (jj < 4) of chunk ch in v[4 ch + jj]: through this column's
     // LDS exchange row to k = 128 ch + 4 l + e; unrolled so that the register indices are static
     double* const xb = reinterpret_cast<double*>(&sm.tile[0][0]) + 128 * w;
-    if (nfc) {   // the lane's own values, k = l + 32 t
-#pragma unroll
-      for (int g = 0; g < kBReg / 4; ++g) {
-        const double a[4] = {v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]};
-        nfscan(a, lane + 128 * g, 32);
-      }
-    }
 #pragma unroll
     for (int ch = 0; ch < kBReg / 4; ++ch) {
       if (ch < ch0 || ch >= ch1) continue;   // column-uniform
@@ -608,14 +625,10 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       chunk(ch, a);
     }
-  } else if (nfc) {   // a summary column: the values only for the summary, zero residues
-    for (int ch = ch0; ch < ch1; ++ch) {
+  } else if (nf) {   // a non-finite column: zero residues, nothing to read
+    for (int ch = c0; ch < c1; ++ch) {
       const int k0 = 128 * ch + 4 * lane;
-      double a[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) a[e] = (k0 + e < K) ? b[k0 + e] : 0.0;
-      nfscan(a, k0, 1);
-      if (k0 < Kp && ch >= c0 && ch < c1)
+      if (k0 < Kp)
         for (int l = 0; l <= N; ++l)
           *(GLOBAL uint32_t*)(B8 + (packed ? packed_offset(j, k0, n, Kp) : (size_t)j * Kp + k0) +
                               (size_t)l * pr.b8_mod_stride) = 0u;
