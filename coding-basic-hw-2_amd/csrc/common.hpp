@@ -164,6 +164,9 @@ int i8_launch(const i8_problem* d_probs, const I8Epi* d_epi, const void* d_sched
 //   words 2 ..: the infinities' positions k, bit 31 set for -Inf (any order)
 // The dot-product pass evaluates the safety-fallback entries of such rows / columns from them.
 constexpr int kNfWords = 16, kNfCap = kNfWords - 2, kNfNoFinite = -2000;
+// nff: zero in every call's descriptors; prep sets it when a row or column of the problem is
+// non-finite (NaN / Inf), and the reconstruct then reads the shifts before the digits, skipping the
+// digits of lanes whose every entry takes the safety fallback.
 struct YDesc {
   const uint8_t* Y;
   size_t y_stride;
@@ -171,6 +174,7 @@ struct YDesc {
   uint64_t* F;
   int32_t* nf;
   int t0, d0;
+  int nff, pad;
 };
 // Compact grids of a grouped call (ne problems): tiles in all and, when every problem has the same
 // count, that count (else 0) -- for the reconstruct and for the dot-product pass.

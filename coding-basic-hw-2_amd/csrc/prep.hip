@@ -237,7 +237,8 @@ __device__ __forceinline__ void nf_header(GLOBAL int32_t* nfw, int ni, int nan, 
 // ------------------------------------------------------------------------------- A rows
 template <bool kWide>
 __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ tab, int blk, int split,
-                          int nsplit, PrepShared& sm, unsigned long long* cnt, int widx, bool packed, int32_t* nfo) {
+                          int nsplit, PrepShared& sm, unsigned long long* cnt, int widx, bool packed, int32_t* nfo,
+                          int* nff) {
   const int tid = threadIdx.x;
   // split 0, when the call asks for summaries: pass 1, which reads every value of the block's rows,
   // also collects each row's non-finite summary state (NaN seen, largest finite magnitude,
@@ -346,7 +347,10 @@ __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ t
     if (valid && split == 0) {
       ((GLOBAL int32_t*)pr.row_shift)[i] = sh;
       ((GLOBAL int32_t*)pr.row_shift)[m + i] = sg;
-      if (sh == OZ2_SHIFT_NONFINITE) atomicAdd(&cnt[0], 1ull);
+      if (sh == OZ2_SHIFT_NONFINITE) {
+        atomicAdd(&cnt[0], 1ull);
+        if (nff) atomicOr(nff, 1);
+      }
     }
   }
   __syncthreads();
@@ -431,7 +435,7 @@ constexpr int kBReg = 32;   // column values per lane held in registers (K <= 32
 
 template <bool kWide>
 __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ tab, int blk, int split,
-                          int nsplit, PrepShared& sm, unsigned long long* cnt, bool packed, int32_t* nfo) {
+                          int nsplit, PrepShared& sm, unsigned long long* cnt, bool packed, int32_t* nfo, int* nff) {
   const int lane = threadIdx.x & 31, w = threadIdx.x >> 5;
   const int j = blk * kBCols + w;
   const int n = pr.n, N = pr.num_moduli, K = pr.k, Kp = pr.kp;
@@ -562,7 +566,10 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
   if (lane == 0 && split == 0) {
     ((GLOBAL int32_t*)pr.col_shift)[j] = sh;
     ((GLOBAL int32_t*)pr.col_shift)[n + j] = sg;
-    if (sh == OZ2_SHIFT_NONFINITE) atomicAdd(&cnt[0], 1ull);
+    if (sh == OZ2_SHIFT_NONFINITE) {
+      atomicAdd(&cnt[0], 1ull);
+      if (nff) atomicOr(nff, 1);
+    }
   }
   const bool nf = sh == OZ2_SHIFT_NONFINITE;
 
@@ -689,6 +696,8 @@ __global__ void __launch_bounds__(kThreads, 4) prep_kernel(const oz2_problem* __
   }
   const oz2_problem& pr = probs[pi];
   int32_t* const nfo = yds ? yds[pi].nf : nullptr;
+  // the problem's non-finite flag (the descriptors are device memory of this call)
+  int* const nff = yds ? const_cast<int*>(&yds[pi].nff) : nullptr;
   const int N = pr.num_moduli;
   if (N < 1 || N > kMaxModuli || pr.alpha == 0.0) return;   // alpha == 0: A, B never referenced
   // folded A residues use the weights q 2^(8 i) mod p, so that sum b_i [q 2^(8 i)] = q x (mod p)
@@ -696,9 +705,9 @@ __global__ void __launch_bounds__(kThreads, 4) prep_kernel(const oz2_problem* __
   const bool packed = pr.kp <= packed_kp;   // packed_kp = 0: row-major (every Kp >= 32)
   if (blk < a_blocks) {
     if (blk * kARows >= pr.m) return;
-    prep_rows<kWide>(pr, tab, blk, blockIdx.z, gridDim.z, sm, cnt, fold ? N : 0, packed, nfo);
+    prep_rows<kWide>(pr, tab, blk, blockIdx.z, gridDim.z, sm, cnt, fold ? N : 0, packed, nfo, nff);
   } else {
-    prep_cols<kWide>(pr, tab, blk - a_blocks, blockIdx.z, gridDim.z, sm, cnt, packed, nfo);
+    prep_cols<kWide>(pr, tab, blk - a_blocks, blockIdx.z, gridDim.z, sm, cnt, packed, nfo, nff);
   }
 }
 

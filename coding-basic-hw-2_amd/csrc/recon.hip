@@ -350,25 +350,43 @@ __global__ void __launch_bounds__(kThreads) recon_kernel(const oz2_problem* __re
       if (kDigits) {
         const YDesc yd = yds[pi];
         const GLOBAL uint8_t* Y = gp(yd.Y) + off;
+        auto digits = [&]() {
 #pragma unroll
-        for (int l = 0; l < kMaxModuli; ++l) {
-          if (l < N) {
-            const GLOBAL uint8_t* y = Y + (size_t)l * yd.y_stride;
-            if (kBlocked || full) {
-              yv[l] = *reinterpret_cast<const GLOBAL uint32_t*>(y);
-            } else {
-              uint32_t v = 0;
-              for (int e = 0; e < ne; ++e) v |= (uint32_t)y[e] << (8 * e);
-              yv[l] = v;
+          for (int l = 0; l < kMaxModuli; ++l) {
+            if (l < N) {
+              const GLOBAL uint8_t* y = Y + (size_t)l * yd.y_stride;
+              if (kBlocked || full) {
+                yv[l] = *reinterpret_cast<const GLOBAL uint32_t*>(y);
+              } else {
+                uint32_t v = 0;
+                for (int e = 0; e < ne; ++e) v |= (uint32_t)y[e] << (8 * e);
+                yv[l] = v;
+              }
             }
           }
-        }
-        const GLOBAL int32_t* L = gp(yd.L) + off;
-        if (kBlocked || full) {
-          const v4i a = *reinterpret_cast<const GLOBAL v4i*>(L);
-          Lv[0] = a.x; Lv[1] = a.y; Lv[2] = a.z; Lv[3] = a.w;
+          const GLOBAL int32_t* L = gp(yd.L) + off;
+          if (kBlocked || full) {
+            const v4i a = *reinterpret_cast<const GLOBAL v4i*>(L);
+            Lv[0] = a.x; Lv[1] = a.y; Lv[2] = a.z; Lv[3] = a.w;
+          } else {
+            for (int e = 0; e < ne; ++e) Lv[e] = L[e];
+          }
+        };
+        if (yd.nff) {   // workgroup-uniform
+          // a problem with non-finite rows / columns: the shifts first, and no digit for a lane
+          // whose every entry takes the safety fallback (its column, or each of its rows, is
+          // non-finite; such entries use neither S1, S2 nor L)
+          bool fin = false;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) fin = fin || (e < ne && rsh[e] != OZ2_SHIFT_NONFINITE);
+          if (fin && csh != OZ2_SHIFT_NONFINITE) {
+            digits();
+          } else {
+#pragma unroll
+            for (int l = 0; l < kMaxModuli; ++l) yv[l] = 0u;
+          }
         } else {
-          for (int e = 0; e < ne; ++e) Lv[e] = L[e];
+          digits();
         }
       } else {
         const GLOBAL int32_t* C32 = gp(pr.C32) + off;
