@@ -51,7 +51,14 @@ const CrtTables* host_tables();
 
 // Process-wide per-device state: the tables and the four sticky counters
 // {nonfinite vectors, uncertified, repaired, safety fallback}.  Created on first use on the
-// current device and kept until the process ends.
+// current device and kept until the process ends.  Each counter is kept in kCounterSlots copies,
+// one 128-byte line per slot (counter q of slot s at s kCounterStride + q): a workgroup adds to the
+// slot of its index, so the one atomic per workgroup and counter does not queue on one address when
+// a call has a hundred thousand workgroups that count; readers sum the slots.
+constexpr int kCounterSlots = 64, kCounterStride = 16;
+__device__ inline unsigned long long* counter_slot(unsigned long long* cnt) {
+  return cnt + ((blockIdx.x + blockIdx.y) % kCounterSlots) * kCounterStride;
+}
 struct DevCtx {
   int device;
   int num_cus;

@@ -234,15 +234,19 @@ extern "C" int oz2_choose_num_moduli_cw(int k, double rho_budget) {
 extern "C" int oz2_read_counters(oz2_counters* out, int reset, hipStream_t s) {
   DevCtx* c = dev_ctx();
   if (!c) return 1;
-  unsigned long long h[4] = {0, 0, 0, 0};
+  // the slots of every counter, summed (the kernels spread their atomics over them)
+  static thread_local unsigned long long h[kCounterSlots * kCounterStride];
   if (out && hipMemcpyAsync(h, c->counters, sizeof h, hipMemcpyDeviceToHost, s) != hipSuccess) return 2;
   if (reset && hipMemsetAsync(c->counters, 0, sizeof h, s) != hipSuccess) return 4;
   if (out) {
     if (hipStreamSynchronize(s) != hipSuccess) return 3;
-    out->nonfinite_vectors = h[0];
-    out->uncertified = h[1];
-    out->repaired = h[2];
-    out->safety_fallback = h[3];
+    unsigned long long v[4] = {0, 0, 0, 0};
+    for (int sl = 0; sl < kCounterSlots; ++sl)
+      for (int q = 0; q < 4; ++q) v[q] += h[sl * kCounterStride + q];
+    out->nonfinite_vectors = v[0];
+    out->uncertified = v[1];
+    out->repaired = v[2];
+    out->safety_fallback = v[3];
   }
   return 0;
 }

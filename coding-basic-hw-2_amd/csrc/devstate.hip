@@ -1,4 +1,5 @@
-// devstate.hip -- per-device resident state: the CRT constants and the four sticky counters are
+// devstate.hip -- per-device resident state: the CRT constants and the four sticky counters (in
+// kCounterSlots slots each) are
 // device globals of this code object (each GPU holds its own copy, zero-filled at load), so setting
 // a device up needs no device allocation -- one copy of the host-built tables into the global.
 #include "common.hpp"
@@ -6,7 +7,7 @@
 namespace ggemm {
 namespace {
 __device__ CrtTables g_tables;
-__device__ unsigned long long g_counters[4];
+__device__ unsigned long long g_counters[kCounterSlots * kCounterStride];
 }  // namespace
 
 int device_state(void** tables, void** counters) {

@@ -348,8 +348,8 @@ __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ t
       ((GLOBAL int32_t*)pr.row_shift)[i] = sh;
       ((GLOBAL int32_t*)pr.row_shift)[m + i] = sg;
       if (sh == OZ2_SHIFT_NONFINITE) {
-        atomicAdd(&cnt[0], 1ull);
-        if (nff) atomicOr(nff, 1);
+        atomicAdd(counter_slot(cnt), 1ull);
+        if (nff) *nff = 1;   // (every writer stores the same value)
       }
     }
   }
@@ -567,8 +567,8 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
     ((GLOBAL int32_t*)pr.col_shift)[j] = sh;
     ((GLOBAL int32_t*)pr.col_shift)[n + j] = sg;
     if (sh == OZ2_SHIFT_NONFINITE) {
-      atomicAdd(&cnt[0], 1ull);
-      if (nff) atomicOr(nff, 1);
+      atomicAdd(counter_slot(cnt), 1ull);
+      if (nff) *nff = 1;
     }
   }
   const bool nf = sh == OZ2_SHIFT_NONFINITE;

@@ -492,7 +492,7 @@ __global__ void __launch_bounds__(kThreads) recon_kernel(const oz2_problem* __re
   if (threadIdx.x < 3) {
     unsigned long long t = 0;
     for (int w = 0; w < kThreads / 64; ++w) t += red[threadIdx.x][w];
-    if (t) atomicAdd(&cnt[1 + threadIdx.x], t);
+    if (t) atomicAdd(counter_slot(cnt) + 1 + threadIdx.x, t);
   }
 }
 
