@@ -174,6 +174,9 @@ constexpr int kNfWords = 16, kNfCap = kNfWords - 2, kNfNoFinite = -2000;
 // nff: zero in every call's descriptors; prep sets it when a row or column of the problem is
 // non-finite (NaN / Inf), and the reconstruct then reads the shifts before the digits, skipping the
 // digits of lanes whose every entry takes the safety fallback.
+// fla: zero in every call's descriptors; the reconstruct sets it when it flags an entry of the
+// problem, and the dot-product pass returns at once for problems without (a replayed graph may
+// find it set from an earlier run: the pass then reads the flags, as always).
 struct YDesc {
   const uint8_t* Y;
   size_t y_stride;
@@ -181,7 +184,7 @@ struct YDesc {
   uint64_t* F;
   int32_t* nf;
   int t0, d0;
-  int nff, pad;
+  int nff, fla;
 };
 // Compact grids of a grouped call (ne problems): tiles in all and, when every problem has the same
 // count, that count (else 0) -- for the reconstruct and for the dot-product pass.

@@ -282,7 +282,7 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
     yd.F = c.blocked ? reinterpret_cast<uint64_t*>(fbase + of) : nullptr;
     yd.nf = nfsum ? reinterpret_cast<int32_t*>(nbase + onf) : nullptr;
     yd.nff = 0;
-    yd.pad = 0;
+    yd.fla = 0;
     {   // compact reconstruct / dot-product grids
       const int rm = c.blocked ? kReconTileMB : kReconTileMC, rn = c.blocked ? kReconTileNB : kReconTileNC;
       const long long rt = (long long)((p.m + rm - 1) / rm) * ((p.n + rn - 1) / rn);

@@ -463,6 +463,7 @@ __global__ void __launch_bounds__(kThreads) recon_kernel(const oz2_problem* __re
       const size_t bidx = (size_t)(cb >> 4) * (size_t)((m + 15) >> 4) + (size_t)(br >> 4);
       GLOBAL uint64_t* F = gpw(yds[pi].F) + 4 * bidx;
       F[0] = f0; F[1] = f1; F[2] = f2; F[3] = f3;
+      if (f0 | f1 | f2 | f3) *const_cast<int*>(&yds[pi].fla) = 1;   // (every writer stores the same value)
     }
   } else {
     many = __syncthreads_count(dmask != 0u) >= kTileDots;
@@ -825,6 +826,7 @@ __global__ void __launch_bounds__(kThreads, 5) dots_kernel(const oz2_problem* __
   const int r0 = (lt % max(tiles_m, 1)) * kRT, c0 = (lt / max(tiles_m, 1)) * kRT;
   // workgroup-uniform: invalid problems, alpha = 0 (no dot product) and tiles past the problem
   if (N < 1 || N > kMaxModuli || m <= 0 || n <= 0 || r0 >= m || c0 >= n || pr.alpha == 0.0) return;
+  if (!yds[pi].fla) return;   // the reconstruct flagged no entry of the problem
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const double alpha = pr.alpha, beta = pr.beta;
   const int mb = (m + 15) >> 4;
