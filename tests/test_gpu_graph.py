@@ -194,3 +194,47 @@ def test_persistent_plan_replays_match_oracle():
     finally:
         G.lib().ggemm_destroy_plan(plan)
         h.close()
+
+
+def test_plan_replays_alternate_nonfinite_and_finite_data():
+    """One plan replayed on a data set with NaN / Inf entries and on a finite one, alternately
+    (ggemm_plan_update_pointers between the runs), repair ON.  Prep marks problems with non-finite
+    rows / columns and the reconstruct marks problems with flagged entries in the plan's device
+    descriptors; a replay on finite data after one on non-finite data sees those marks still set
+    and must take the general paths, so every run is compared with the oracle bit for bit."""
+    shapes = [(200, 150, 300)] * 2 + [(64, 96, 1200), (130, 70, 40)]
+    X = Case(shapes, 81, phi=2.0, alpha=1.5, beta=0.5)
+    Y = Case(shapes, 82, phi=1.0, alpha=1.5, beta=0.5)
+    rng = np.random.default_rng(83)
+    for hp in X.hp:
+        for arr, rows, cols, ld in ((hp.A, hp.m, hp.k, hp.lda), (hp.B, hp.k, hp.n, hp.ldb)):
+            nbad = max(1, rows * cols // 1500)
+            arr[rng.integers(0, rows, nbad) + rng.integers(0, cols, nbad) * ld] = rng.choice(
+                [np.nan, np.inf, -np.inf], nbad)
+    X.alloc()
+    cfg = G.Config(0, 1e-15, 0, G.REPAIR_ON)
+    rc, plan_o = oracle_plan(X, cfg, G.PATH_EMU_GROUPED)
+    assert rc == 0
+    want = {}
+    for name, case in (("X", X), ("Y", Y)):
+        want[name] = [hp.emulate(O.REPAIR_ON, e.num_moduli) for hp, e in zip(case.hp, plan_o)]
+    assert sum(int(c[3]) for _, c in want["X"]) > 0 and sum(int(c[3]) for _, c in want["Y"]) == 0
+    h = G.Handle(len(shapes), *[max(a, b) for a, b in zip(X.sizes(), Y.sizes())])
+    arr = G.problems_array(X.problems())
+    err = C.c_int(0)
+    plan = G.lib().ggemm_make_plan_ex(h.h, G.PATH_EMU_GROUPED, C.byref(cfg), arr, len(shapes), C.byref(err))
+    assert plan, err.value
+    ptr = lambda ts: (C.c_void_p * len(shapes))(*[t.data_ptr() for t in ts])
+    try:
+        for rep, name in enumerate(("X", "Y", "Y", "X", "Y")):
+            case = X if name == "X" else Y
+            case.reset_C()
+            assert G.lib().ggemm_plan_update_pointers(plan, ptr(case.dA), ptr(case.dB), ptr(case.dC)) == 0
+            say(f"plan replay {rep} on {name}")
+            assert G.lib().ggemm_execute_plan(plan, None) == 0
+            torch.cuda.synchronize()
+            for g, (Co, _) in enumerate(want[name]):
+                assert same_bits(case.C(g), Co), f"replay {rep} ({name}): problem {g} differs"
+    finally:
+        G.lib().ggemm_destroy_plan(plan)
+        h.close()
