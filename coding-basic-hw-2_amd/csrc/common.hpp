@@ -206,10 +206,11 @@ int f64_build_schedule(const F64Problem* h, int num, void* h_ws, size_t ws_bytes
 int f64_launch(const F64Problem* d_probs, const void* d_sched, int launch, hipStream_t s);
 
 // Launchers used by the orchestration (return 0 on success).
-// fold_q != 0: the residues of A plane l are (q_l r) mod p_l (symmetric) instead of r, with q_l the
-// CRT inverse of modulus l for the problem's N; the abs plane and B are unchanged.
-// fold_q: A residues carry the CRT inverses (production); packed_kp: the residue planes of problems
-// with Kp <= packed_kp are in the packed layout, the others row-major (0: every problem row-major)
+// fold_q != 0 (production): the residues of A plane l are (q_l r) mod p_l (symmetric) instead of r,
+// with q_l the CRT inverse of modulus l for the problem's N (the abs plane and B are unchanged), and
+// the planes of non-finite rows / columns are left unwritten; fold_q = 0: plain residues, zeros for
+// non-finite rows / columns.
+// packed_kp: the residue planes of problems with Kp <= packed_kp are in the packed layout, the others row-major (0: every problem row-major)
 // max_moduli: the largest num_moduli among the num problems (selects the digit width)
 // yd (or nullptr): descriptors parallel to d whose nf summaries prep writes
 // order (or nullptr: 0 .. num - 1): the problems in the order their workgroups are dispatched

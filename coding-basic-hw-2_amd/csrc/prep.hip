@@ -238,7 +238,7 @@ __device__ __forceinline__ void nf_header(GLOBAL int32_t* nfw, int ni, int nan, 
 template <bool kWide>
 __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ tab, int blk, int split,
                           int nsplit, PrepShared& sm, unsigned long long* cnt, int widx, bool packed, int32_t* nfo,
-                          int* nff) {
+                          int* nff, bool zero_nf) {
   const int tid = threadIdx.x;
   // split 0, when the call asks for summaries: pass 1, which reads every value of the block's rows,
   // also collects each row's non-finite summary state (NaN seen, largest finite magnitude,
@@ -368,7 +368,10 @@ __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ t
   const int ntile = (Kp + kATile - 1) / kATile;
   const int per = (ntile + nsplit - 1) / nsplit;
   const int w0 = min(ntile, split * per), w1 = min(ntile, w0 + per);   // tiles written here
-  const int l0 = split == 0 ? 0 : w0, l1 = split == 0 ? ntile : w1;   // tiles walked here
+  int l0 = split == 0 ? 0 : w0, l1 = split == 0 ? ntile : w1;   // tiles walked here
+  // without zero residues, a block whose every row is non-finite has nothing to walk (its rows'
+  // sums stay 0, as the walk leaves them)
+  if (!zero_nf && __syncthreads_and(!valid || nf_c)) l1 = l0;
   for (int t = l0; t < l1; ++t) {
     const int k0 = t * kATile;
     double av[kATile / kChains];
@@ -395,8 +398,9 @@ __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ t
     if (t >= w0 && t < w1 && rvalid && kb < Kp) {
       GLOBAL int8_t* dst = (GLOBAL int8_t*)pr.A8 + (packed ? packed_offset(row0 + rr, kb, m, Kp) : (size_t)(row0 + rr) * Kp + kb);
       if (nf_r) {
-        for (int l = 0; l <= N; ++l)
-          *(GLOBAL u32x4*)(dst + (size_t)l * pr.a8_mod_stride) = u32x4{0u, 0u, 0u, 0u};
+        if (zero_nf)
+          for (int l = 0; l <= N; ++l)
+            *(GLOBAL u32x4*)(dst + (size_t)l * pr.a8_mod_stride) = u32x4{0u, 0u, 0u, 0u};
       } else {
         double av[16], xt[16];
 #pragma unroll
@@ -435,7 +439,8 @@ constexpr int kBReg = 32;   // column values per lane held in registers (K <= 32
 
 template <bool kWide>
 __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ tab, int blk, int split,
-                          int nsplit, PrepShared& sm, unsigned long long* cnt, bool packed, int32_t* nfo, int* nff) {
+                          int nsplit, PrepShared& sm, unsigned long long* cnt, bool packed, int32_t* nfo, int* nff,
+                          bool zero_nf) {
   const int lane = threadIdx.x & 31, w = threadIdx.x >> 5;
   const int j = blk * kBCols + w;
   const int n = pr.n, N = pr.num_moduli, K = pr.k, Kp = pr.kp;
@@ -589,7 +594,7 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
     GLOBAL int8_t* const base = B8 + (packed ? packed_offset(j, k0, n, Kp) : (size_t)j * Kp + k0);
     const bool write = ch >= c0 && ch < c1;
     if (nf) {
-      if (write)
+      if (write && zero_nf)
         for (int l = 0; l <= N; ++l) *(GLOBAL uint32_t*)(base + (size_t)l * pr.b8_mod_stride) = 0u;
       return;
     }
@@ -632,8 +637,8 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       chunk(ch, a);
     }
-  } else if (nf) {   // a non-finite column: zero residues, nothing to read
-    for (int ch = c0; ch < c1; ++ch) {
+  } else if (nf) {   // a non-finite column: zero residues (when asked for), nothing to read
+    for (int ch = c0; ch < (zero_nf ? c1 : c0); ++ch) {
       const int k0 = 128 * ch + 4 * lane;
       if (k0 < Kp)
         for (int l = 0; l <= N; ++l)
@@ -703,11 +708,16 @@ __global__ void __launch_bounds__(kThreads, 4) prep_kernel(const oz2_problem* __
   // folded A residues use the weights q 2^(8 i) mod p, so that sum b_i [q 2^(8 i)] = q x (mod p)
   const bool fold = fold_q && blk < a_blocks;
   const bool packed = pr.kp <= packed_kp;   // packed_kp = 0: row-major (every Kp >= 32)
+  // the residues of a non-finite row / column: zeros for the kernel-level API (fold_q = 0), which
+  // hands the planes over; the grouped pipeline (fold_q = 1) leaves them unwritten, since every
+  // entry in such a row or column takes the safety fallback, which uses neither its digits nor its
+  // L (the GEMM's int32 sums over whatever bytes the planes hold are dropped with those entries)
+  const bool zero_nf = !fold_q;
   if (blk < a_blocks) {
     if (blk * kARows >= pr.m) return;
-    prep_rows<kWide>(pr, tab, blk, blockIdx.z, gridDim.z, sm, cnt, fold ? N : 0, packed, nfo, nff);
+    prep_rows<kWide>(pr, tab, blk, blockIdx.z, gridDim.z, sm, cnt, fold ? N : 0, packed, nfo, nff, zero_nf);
   } else {
-    prep_cols<kWide>(pr, tab, blk - a_blocks, blockIdx.z, gridDim.z, sm, cnt, packed, nfo, nff);
+    prep_cols<kWide>(pr, tab, blk - a_blocks, blockIdx.z, gridDim.z, sm, cnt, packed, nfo, nff, zero_nf);
   }
 }
 
