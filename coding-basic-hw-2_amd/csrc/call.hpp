@@ -49,9 +49,10 @@ int counters_read(ggemm_handle_t h, hipStream_t s, ggemm_stats_t* st);
 // Plans nothing: takes the planner output and fills descriptors + schedules into hb (capacity
 // cap), and the stats fields num_fallback / moduli_* / reuse_* / num_unique_*.  emu_idx and
 // nat_idx are caller scratch of >= num ints.  Returns GGEMM_OK, WORKSPACE, INVALID or I8GEMM.
+// db: the device blob hb is copied to (descriptors that point into the blob address it there).
 // rp: operand-reuse plan (path EMU_GROUPED_REUSE) or nullptr
 int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const ggemm_plan_entry_t* plan,
-                  int* emu_idx, int* nat_idx, char* hb, size_t cap, GroupedCall* out, ggemm_stats_t* st,
+                  int* emu_idx, int* nat_idx, char* hb, const char* db, size_t cap, GroupedCall* out, ggemm_stats_t* st,
                   const reuse_plan* rp = nullptr);
 // Enqueues prep -> INT8 GEMM -> reconstruct (if ne > 0) and the native FP64 GEMM (if nn > 0) on s,
 // reading descriptors from the device blob db.  *launches += kernels issued.  prof_set: stage

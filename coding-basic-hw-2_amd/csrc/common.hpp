@@ -125,8 +125,15 @@ __host__ __device__ inline size_t packed_offset(int row, int k, int rows, int kp
   const int rb = b == (kp >> 6) ? 32 : 64;
   return (size_t)b * (size_t)rows * 64 + (size_t)row * rb + (size_t)(k & 63);
 }
+// rs, cs, nf (or all nullptr): the product's row / column shifts (the first m / n int32 of prep's
+// row_shift, col_shift) and its non-finite flag (YDesc::nff).  When prep has set the flag, a tile
+// whose rows, or whose columns, all carry OZ2_SHIFT_NONFINITE is not computed: each of its entries
+// takes the safety fallback, which uses none of the tile's outputs.
 struct I8Epi {
   uint32_t mode, p, mc, bias;
+  const int32_t* rs;
+  const int32_t* cs;
+  const int* nf;
 };
 I8Epi i8_epi_residue(uint32_t p, int kp);
 __host__ __device__ inline size_t blocked_plane_entries(int m, int n) {

@@ -9,6 +9,7 @@
 // take a native route.
 #include <algorithm>
 #include <cmath>
+#include <cstddef>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -142,8 +143,8 @@ int large_mode(ggemm_handle_t h, const GroupedCall& c) {
 }
 
 int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const ggemm_plan_entry_t* plan,
-                  int* emu_idx, int* nat_idx, char* hb, size_t cap, GroupedCall* out, ggemm_stats_t* st,
-                  const reuse_plan* rp) {
+                  int* emu_idx, int* nat_idx, char* hb, const char* db, size_t cap, GroupedCall* out,
+                  ggemm_stats_t* st, const reuse_plan* rp) {
   GroupedCall c;
   int nmax = 0, pmax = 0;
   size_t SA = 0, SB = 0, SC = 0, rows = 0, cols = 0;
@@ -313,6 +314,9 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
       }
       if (c.blocked) hepi[q].mode |= kEpiBlocked;
       if ((int)kp <= c.packed_kp) hepi[q].mode |= kEpiPacked;
+      hepi[q].rs = o.row_shift;
+      hepi[q].cs = o.col_shift;
+      hepi[q].nf = reinterpret_cast<const int*>(db + c.L.off_yd + j * sizeof(YDesc) + offsetof(YDesc, nff));
     }
     const size_t plane = c.blocked ? blocked_plane_entries(p.m, p.n) : (size_t)p.m * p.n;
     oy += align_up(plane, kBufAlign);
@@ -530,7 +534,7 @@ int path_emu_loop(ggemm_handle_t h, bool batched, const ggemm_problem_t* probs, 
   if ((r = acquire_slot(h, &slot))) return r;
   char* hb = host_slot(h, slot);
   char* db = static_cast<char*>(h->d_desc);
-  r = build_grouped(h, probs, num, h->plan, h->emu_idx, h->nat_idx, hb, h->desc_bytes, &c, st);
+  r = build_grouped(h, probs, num, h->plan, h->emu_idx, h->nat_idx, hb, db, h->desc_bytes, &c, st);
   if (r) { release_slot(h, slot); return r; }
   // per-problem (or per-plane) schedule images after the grouped layout
   const size_t per = batched ? sched_img(kMaxPlanes) : sched_img(1);
@@ -627,7 +631,8 @@ int path_emu(ggemm_handle_t h, ggemm_path_t path, const ggemm_config_t* cfg, con
   char* hb = host_slot(h, slot);
   char* db = static_cast<char*>(h->d_desc);
   GroupedCall c;
-  r = build_grouped(h, probs, num, h->plan, h->emu_idx, h->nat_idx, hb, h->desc_bytes, &c, st, reuse ? &rp : nullptr);
+  r = build_grouped(h, probs, num, h->plan, h->emu_idx, h->nat_idx, hb, db, h->desc_bytes, &c, st,
+                    reuse ? &rp : nullptr);
   if (!r && c.h2d_bytes && hipMemcpyAsync(db, hb, c.h2d_bytes, hipMemcpyHostToDevice, h->stream) != hipSuccess)
     r = GGEMM_ERR_CUDA;
   if (!r) r = enqueue_grouped(c, db, h->stream, repair, &st->kernel_launches, prof::begin());

@@ -76,7 +76,8 @@ int build(ggemm_plan_t p, ggemm_path_t path, const ggemm_config_t* cfg) {
   std::memset(p->h_blob, 0, p->blob_bytes);
   ggemm_stats_t& st = p->st;
   st.num_problems = p->num;
-  r = build_grouped(h, p->probs, p->num, p->entries, p->emu_idx, p->nat_idx, p->h_blob, p->blob_bytes, &p->call, &st);
+  r = build_grouped(h, p->probs, p->num, p->entries, p->emu_idx, p->nat_idx, p->h_blob,
+                    static_cast<const char*>(p->d_blob), p->blob_bytes, &p->call, &st);
   if (r) return r;
   st.num_repaired = st.num_uncertified = st.num_safety_fallback = -1;   // filled per execute
   HIPC(hipMemcpyAsync(p->d_blob, p->h_blob, p->call.h2d_bytes ? p->call.h2d_bytes : 1, hipMemcpyHostToDevice,

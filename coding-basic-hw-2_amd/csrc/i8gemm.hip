@@ -91,13 +91,16 @@ using Cfg0 = Cfg<0, 256, 128, 4, 2, 3>;
 using Cfg1 = Cfg<1, 128, 128, 4, 2, 3>;
 using Cfg2 = Cfg<2, 64, 64, 4, 2, 3>;
 constexpr int kThreads = 512;
-constexpr int kSmem = Cfg0::SMEM;
+// after a configuration's ring: the tile's row shifts (256 int) then its column shifts (256 int),
+// for the non-finite check
+constexpr int kTileCheckBytes = 2048;
+constexpr int kSmem = Cfg0::SMEM + kTileCheckBytes;
 static_assert(Cfg1::SMEM <= kSmem && Cfg2::SMEM <= kSmem, "smem");
 // large-tile kernel: 1024 threads = 16 waves of 64 x 64 (4 per SIMD, so one wave's LDS reads and
 // barrier waits overlap the others' MFMAs), one workgroup per compute unit, 128 KB ring
 using CfgL = Cfg<0, 256, 256, 4, 4, 4>;
 constexpr int kThreadsL = CfgL::NT;
-constexpr int kSmemL = CfgL::SMEM;
+constexpr int kSmemL = CfgL::SMEM + kTileCheckBytes;
 
 __device__ __forceinline__ int swz(int row, int ch) { return ch ^ ((row >> 1) & 3); }
 
@@ -353,6 +356,13 @@ struct TileSrc {
                    wave, lane);
     }
   }
+  // stage kt by the general form only: VM DMA instructions per wave with no branch between them
+  // and the ones of the next stage (the count the tile check's wait relies on)
+  __device__ __forceinline__ void load_general(int kt, uint8_t* st) const {
+    const int k0 = kt * kBK;
+    dma_stage<C>(stage_src(A, m, row0, kp, k0, kPacked), stage_src(B, n, col0, kp, k0, kPacked), m_rem, n_rem, st,
+                 wave, lane);
+  }
   // the stages a tile's k loop expects in flight when it starts (ring slots 0, 1, ...): NST with the
   // split loop, NST - 1 otherwise
   __device__ __forceinline__ void prologue(uint8_t* lds) const {
@@ -365,7 +375,7 @@ struct TileSrc {
 };
 
 __device__ __forceinline__ I8Epi epi_of(const I8Epi* __restrict__ epis, int pi) {
-  return epis ? epis[pi] : I8Epi{0u, 1u, 0u, 0u};
+  return epis ? epis[pi] : I8Epi{0u, 1u, 0u, 0u, nullptr, nullptr, nullptr};
 }
 
 // A unit of the persistent schedule, decoded: one tile (tm, tn) of product pi (< 0: none).
@@ -675,10 +685,54 @@ __device__ __forceinline__ int dispatched_unit(const int* __restrict__ sched) {
   const int x = b % kXcds, q = b / kXcds;
   return (q / CH) * span + x * CH + (q % CH);
 }
+// With the product's shifts given (epi.nf) and its non-finite flag set by prep, a tile whose rows
+// or whose columns are all non-finite is dropped: every entry of it takes the safety fallback.
+// Only on tiles of at least PRE stages.  Each wave DMAs 64 of the tile's row shifts and 64 of its
+// column shifts (indices clamped to the product: a clamped copy is the last row / column, which is
+// in the tile) to LDS after the ring, ahead of the first PRE stages, which are issued in the general
+// form (VM DMA instructions per wave and stage, no branch between them).  With the flag set (a
+// scalar load, landed by then), waiting until PRE VM DMA instructions are outstanding leaves those
+// stages in flight; every wave then reads all the shifts and reaches the same verdict.  Without the
+// flag the shift DMAs are only older operations ahead of the ring's own waits.
 template <class C, bool kPacked>
 __device__ __forceinline__ void one_tile(uint8_t* lds, const i8_problem* __restrict__ probs,
                                          const I8Epi* __restrict__ epis, const Unit& t) {
-  TileSrc<C, kPacked>(probs[t.pi], t.tm, t.tn).prologue(lds);
+  static_assert(C::BM % 64 == 0 && C::BN % 64 == 0 && C::BM <= 256 && C::BN <= 256, "shift rows");
+  static_assert(C::NW >= C::BM / 64 && C::NW >= C::BN / 64, "one shift DMA per wave and operand");
+  constexpr int PRE = C::kSplit ? C::NST : C::NST - 1;
+  const i8_problem& P = probs[t.pi];
+  const TileSrc<C, kPacked> src(P, t.tm, t.tn);
+  const I8Epi e = epi_of(epis, t.pi);
+  if (e.nf != nullptr && P.kp > (PRE - 1) * kBK) {   // workgroup-uniform
+    // written by prep, an earlier kernel of the call, and constant here: a scalar load
+    const int nff = *(const __attribute__((address_space(4))) int*)e.nf;
+    const int lane = src.lane, wave = src.wave;
+    uint8_t* const chk = lds + C::SMEM;
+    const int wr = wave % (C::BM / 64), wc = wave % (C::BN / 64);
+    const int r = min(src.row0 + 64 * wr + lane, P.m - 1), c = min(src.col0 + 64 * wc + lane, P.n - 1);
+    __builtin_amdgcn_global_load_lds((const void*)(e.rs + r), GGEMM_LDS(chk + 256 * wr), 4, 0, 0);
+    __builtin_amdgcn_global_load_lds((const void*)(e.cs + c), GGEMM_LDS(chk + 1024 + 256 * wc), 4, 0, 0);
+#pragma unroll
+    for (int q = 0; q < PRE; ++q) src.load_general(q, lds + q * C::STAGE);
+    if (nff) {
+      wait_barrier<PRE * C::VM>();   // every wave's shift DMAs have landed
+      const uint32_t base = (uint32_t)(uintptr_t)GGEMM_LDS(chk) + 16 * lane;
+      v4i sr = lds_read<0>(base), sc = lds_read<1024>(base);
+      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(sr), "+v"(sc));
+      bool fr = false, fc = false;
+#pragma unroll
+      for (int x = 0; x < 4; ++x) {
+        fr = fr || (4 * lane + x < C::BM && sr[x] != OZ2_SHIFT_NONFINITE);
+        fc = fc || (4 * lane + x < C::BN && sc[x] != OZ2_SHIFT_NONFINITE);
+      }
+      if (__ballot(fr) == 0 || __ballot(fc) == 0) {   // no finite row, or no finite column
+        wait_barrier<0>();   // the stages have landed before the workgroup ends
+        return;
+      }
+    }
+  } else {
+    src.prologue(lds);
+  }
   run_tile<C, kPacked, true>(lds, probs, epis, t.pi, t.tm, t.tn, [] {}, [] { return Unit{-1, 0, 0, 0}; });
 }
 

@@ -137,12 +137,12 @@ extern "C" int ggemm_grouped_dgemm_noalloc(ggemm_path_t path, const ggemm_config
   r = ggemm_plan_ex(problems, num_problems, cfg, path, &h->dm, h->plan, h->plan_memo, h->plan_memo_cap);
   if (r) return r;
   GroupedCall c;
-  r = build_grouped(h, problems, num_problems, h->plan, h->emu_idx, h->nat_idx, g_blob, h->desc_bytes, &c, st);
+  char* db = static_cast<char*>(h->d_desc);   // this device's scratch address
+  r = build_grouped(h, problems, num_problems, h->plan, h->emu_idx, h->nat_idx, g_blob, db, h->desc_bytes, &c, st);
   if (r) {
     if (r == GGEMM_ERR_WORKSPACE) report_limits("call exceeds the static workspace");
     return r;
   }
-  char* db = static_cast<char*>(h->d_desc);
   if (c.h2d_bytes) {
     // the source is static host memory that the next call rewrites: wait for the copy to land
     if (hipMemcpyAsync(db, g_blob, c.h2d_bytes, hipMemcpyHostToDevice, stream) != hipSuccess ||

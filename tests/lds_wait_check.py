@@ -1,11 +1,14 @@
-"""Checks a kernel's AMDGPU assembly for uses of VGPRs whose LDS load (ds_read*) may still be pending.
+"""Checks a kernel's AMDGPU assembly for uses of VGPRs whose LDS load (ds_read*) or vector-memory
+load (global_ / buffer_ / flat_ / scratch_ loads, returning atomics) may still be pending.
 
-The INT8 GEMM issues its fragment reads as inline assembly and waits for them with an explicit
-s_waitcnt, so the compiler cannot see the dependency: a register copy it placed between a read
-and its wait would read stale data.  Dataflow over the control-flow graph: state = the pending
-LDS-load destination register sets, oldest first; s_waitcnt lgkmcnt(N) keeps only the newest N
-(LDS completes in order; scalar loads do not, so the N outstanding may all be LDS).  Any other
-instruction that names a pending register is reported.
+The INT8 GEMM issues its fragment reads, and the shift loads of its tile check, as inline assembly
+and waits for them with an explicit s_waitcnt, so the compiler cannot see the dependency: a
+register copy it placed between a load and its wait would read stale data.  Dataflow over the
+control-flow graph: state = the pending LDS-load destination register sets and the pending
+vector-memory operations (their destination sets, empty for stores and LDS DMA), oldest first;
+s_waitcnt lgkmcnt(N) keeps only the newest N LDS entries (LDS completes in order; scalar loads do
+not, so the N outstanding may all be LDS), vmcnt(N) the newest N vector-memory entries (they
+complete in order).  Any other instruction that names a pending register is reported.
 Usage: python3 lds_wait_check.py file.s kernel_symbol_substring   (exit status 1 on a finding)
 """
 import re
@@ -29,6 +32,8 @@ def _merge(a, b):
 
 
 def _blocks(lines):
+    """Instructions per branch-target label (blocks labelled only by a comment stay merged into the
+    preceding one: their branches are followed where they stand)."""
     blocks, order, cur = {"__entry": []}, ["__entry"], "__entry"
     for ln in lines:
         m = re.match(r"^(\.LBB\w+|\S+):", ln)
@@ -40,22 +45,28 @@ def _blocks(lines):
         t = ln.split(";")[0].strip()
         if t and not t.startswith("."):
             blocks[cur].append(t)
-    succ = {}
-    for bi, b in enumerate(order):
-        s, fall = [], True
-        for t in blocks[b]:
-            op = t.split()[0]
-            if op == "s_branch":
-                s.append(t.split()[1])
-                fall = False
-            elif op.startswith("s_cbranch"):
-                s.append(t.split()[1])
-            elif op in ("s_endpgm", "s_setpc_b64"):
-                fall = False
-        if fall and bi + 1 < len(order):
-            s.append(order[bi + 1])
-        succ[b] = s
-    return blocks, order, succ
+    return blocks, order
+
+
+def _vmem(op, t):
+    """(is a vector-memory operation, its destination text or None)."""
+    if not op.startswith(("global_", "buffer_", "flat_", "scratch_")):
+        return False, None
+    parts = t[len(op):].split(",")
+    if "_load" in op and "_lds" not in op:
+        return True, parts[0]
+    if "_atomic" in op and re.search(r"\b(sc0|glc)\b", t):   # returns the old value
+        return True, parts[0]
+    return True, None
+
+
+# counter widths on gfx9: at most this many operations outstanding, so older entries have completed
+# (the cap also bounds the dataflow state in loops that never drain)
+kVmMax, kLgkmMax = 63, 15
+
+
+def _keep(st, n):
+    return [] if n == 0 else st[max(0, len(st) - n):]
 
 
 def check_lines(src, want):
@@ -63,40 +74,68 @@ def check_lines(src, want):
     start = next(i for i, ln in enumerate(src)
                  if not ln.startswith("\t") and re.match(r"^\S*" + re.escape(want) + r"\S*:", ln))
     end = next(i for i in range(start, len(src)) if "s_endpgm" in src[i])
-    blocks, order, succ = _blocks(src[start + 1:end + 1])
+    blocks, order = _blocks(src[start + 1:end + 1])
     state_in = {b: None for b in order}
-    state_in["__entry"] = []
+    state_in["__entry"] = ([], [])
     work, reports = ["__entry"], set()
+
+    def flow(target, lg, vm):   # the state reaching target along one edge
+        if target not in state_in:
+            return
+        old = state_in[target]
+        new = (lg, vm) if old is None else (_merge(old[0], lg), _merge(old[1], vm))
+        if old is None or new != old:
+            state_in[target] = new
+            work.append(target)
+
     while work:
         b = work.pop()
-        st = [set(x) for x in state_in[b]]
+        lg = [set(x) for x in state_in[b][0]]
+        vm = [set(x) for x in state_in[b][1]]
+        live = True
         for t in blocks[b]:
             op = t.split()[0]
             rest = t[len(op):]
             if op == "s_waitcnt":
                 m = re.search(r"lgkmcnt\((\d+)\)", t)
                 if m:
-                    n = int(m.group(1))
-                    st = [] if n == 0 else st[max(0, len(st) - n):]
+                    lg = _keep(lg, int(m.group(1)))
+                m = re.search(r"vmcnt\((\d+)\)", t)
+                if m:
+                    vm = _keep(vm, int(m.group(1)))
                 continue
-            pend = set().union(*st) if st else set()
+            if op.startswith("s_cbranch"):
+                flow(t.split()[1], lg, vm)
+                continue
+            if op == "s_branch":
+                flow(t.split()[1], lg, vm)
+                live = False
+                break
+            if op in ("s_endpgm", "s_setpc_b64"):
+                live = False
+                break
+            pend = set().union(*lg, *vm)
             if op.startswith("ds_read") or op.startswith("ds_load"):
                 parts = rest.split(",")
                 srcs = _regs(",".join(parts[1:]))
                 if srcs & pend:
                     reports.add((b, t, tuple(sorted(srcs & pend))))
-                st.append(_regs(parts[0]))
+                lg = _keep(lg + [_regs(parts[0])], kLgkmMax)
+                continue
+            is_vm, dst = _vmem(op, t)
+            if is_vm:
+                parts = rest.split(",")
+                srcs = _regs(",".join(parts[1:]) if dst is not None else rest)
+                if srcs & pend:
+                    reports.add((b, t, tuple(sorted(srcs & pend))))
+                vm = _keep(vm + [_regs(dst) if dst is not None else set()], kVmMax)
                 continue
             used = _regs(rest)
             if used & pend:
                 reports.add((b, t, tuple(sorted(used & pend))))
-        for s2 in succ[b]:
-            if s2 not in state_in:
-                continue
-            new = st if state_in[s2] is None else _merge(state_in[s2], st)
-            if state_in[s2] is None or new != state_in[s2]:
-                state_in[s2] = new
-                work.append(s2)
+        bi = order.index(b)
+        if live and bi + 1 < len(order):
+            flow(order[bi + 1], lg, vm)
     return sorted(reports)
 
 
@@ -109,5 +148,5 @@ if __name__ == "__main__":
     found = check(sys.argv[1], sys.argv[2])
     for b, t, r in found:
         print(f"{b}: {t}   pending {r[:8]}")
-    print(f"{len(found)} uses of pending LDS destinations")
+    print(f"{len(found)} uses of pending load destinations")
     sys.exit(1 if found else 0)

@@ -1,7 +1,8 @@
-"""The INT8 GEMM's fragment reads are inline-assembly LDS loads whose waits the compiler cannot
-see.  Compile csrc/i8gemm.hip for gfx950 and check, by dataflow over each kernel's assembly, that
-no instruction uses a fragment register before the s_waitcnt that covers its load (CPU only).
-The checker itself is tested on a hand-written fragment with one such use."""
+"""The INT8 GEMM's fragment reads (LDS) and its tile check's shift loads (global) are inline-assembly
+loads whose waits the compiler cannot see.  Compile csrc/i8gemm.hip for gfx950 and check, by
+dataflow over each kernel's assembly, that no instruction uses such a register before the
+s_waitcnt that covers its load (CPU only).  The checker itself is tested on hand-written fragments
+with one such use."""
 import subprocess
 from pathlib import Path
 
@@ -21,6 +22,26 @@ def test_checker_finds_a_stale_read():
     asm2 = ["k:", "\tds_read_b128 v[10:13], v1", "\tds_read_b128 v[14:17], v1 offset:64", "\ts_waitcnt lgkmcnt(1)",
             "\tv_mov_b32 v20, v11", "\tv_mov_b32 v21, v15", "\ts_endpgm"]
     assert [t for _, t, _ in L.check_lines(asm2, "k")] == ["v_mov_b32 v21, v15"]
+
+
+def test_checker_finds_a_pending_global_load():
+    """A global load ahead of two LDS DMAs: vmcnt(2) covers it, vmcnt(3) does not."""
+    def asm(n):
+        return ["k:", "\tglobal_load_dword v7, v[2:3], off", "\tglobal_load_lds_dwordx4 v[4:5], off",
+                "\tglobal_load_lds_dwordx4 v[4:5], off", f"\ts_waitcnt vmcnt({n})", "\tv_cmp_ne_u32_e32 vcc, 0, v7",
+                "\ts_endpgm"]
+    assert L.check_lines(asm(2), "k") == []
+    assert [t for _, t, _ in L.check_lines(asm(3), "k")] == ["v_cmp_ne_u32_e32 vcc, 0, v7"]
+
+
+def test_checker_finds_a_pending_global_load():
+    """A global load ahead of two LDS DMAs: vmcnt(2) covers it, vmcnt(3) does not."""
+    def asm(n):
+        return ["k:", "\tglobal_load_dword v7, v[2:3], off", "\tglobal_load_lds_dwordx4 v[4:5], off",
+                "\tglobal_load_lds_dwordx4 v[4:5], off", f"\ts_waitcnt vmcnt({n})", "\tv_cmp_ne_u32_e32 vcc, 0, v7",
+                "\ts_endpgm"]
+    assert L.check_lines(asm(2), "k") == []
+    assert [t for _, t, _ in L.check_lines(asm(3), "k")] == ["v_cmp_ne_u32_e32 vcc, 0, v7"]
 
 
 def test_int8_gemm_kernels_wait_before_use(tmp_path):

@@ -403,6 +403,42 @@ def test_hard_numerics_nan_inf_and_repair():
     check_case(case, G.PATH_AUTO, CFG_AUTO, st, O.REPAIR_ON)
 
 
+@pytest.mark.parametrize("sched", ["dispatch", "persistent"])
+@pytest.mark.parametrize("kernel", ["large", "general"])
+def test_nonfinite_tiles_skipped(kernel, sched):
+    """INT8 GEMM tiles whose rows (or columns) are all non-finite are not computed by the
+    dispatched kernels (every entry takes the safety fallback); the persistent kernels compute
+    them.  Either way the bits and counters are the oracle's: a problem with a non-finite value
+    in every A row, one whose first 256 B columns are non-finite (later columns finite), one whose
+    first 256 A rows are non-finite, a short-k problem with every row non-finite (below the
+    check's stage count), and a finite problem."""
+    case = Case([(300, 200, 400), (260, 300, 300), (512, 96, 500), (100, 90, 100), (128, 128, 256)],
+                20261206, phi=2.0)
+    rng = np.random.default_rng(6)
+    bad = [np.nan, np.inf, -np.inf]
+
+    def spoil_rows(h, rows):   # one non-finite value in each given row of A
+        for i in rows:
+            h.A[i + rng.integers(0, h.k) * h.lda] = bad[i % 3]
+
+    spoil_rows(case.hp[0], range(300))
+    for j in range(256):   # one non-finite value in each of the first 256 columns of B
+        h = case.hp[1]
+        h.B[rng.integers(0, h.k) + j * h.ldb] = bad[j % 3]
+    spoil_rows(case.hp[2], range(256))
+    spoil_rows(case.hp[3], range(100))
+    case.alloc()
+    say(f"non-finite tiles, {kernel} kernel, {sched}")
+    env = {"GGEMM_I8_SCHED": "persistent"} if sched == "persistent" else {}
+    run_kernel(case, kernel, **env)
+    say("non-finite tiles, default kernel, repair ON")
+    cfg = G.Config(0, 1e-15, 1, G.REPAIR_ON)
+    rc, st = run(case, G.PATH_EMU_GROUPED, cfg)
+    assert rc == 0
+    tot = check_case(case, G.PATH_EMU_GROUPED, cfg, st, O.REPAIR_ON)
+    assert tot[3] == 300 * 200 + 256 * 260 + 256 * 96 + 100 * 90
+
+
 def env_handle(case, min_k=None, **env):
     """A handle created with environment variables set (read at creation)."""
     saved = dict(os.environ)
