@@ -306,7 +306,26 @@ def main():
     i8_kernel = G.lib().ggemm_profile_i8_kernel().decode()
     st_ms = [stage[q] / max(ncalls.value, 1) for q in range(4)]
     i8_ms = st_ms[1]
-    achieved = int8_ops / (i8_ms * 1e-3) / 1e12 if i8_ms > 0 else 0.0
+    # with non-finite data the dispatched INT8 kernels skip tiles that have no finite row or no
+    # finite column (their entries all take the safety fallback): the roofline counts the
+    # operations of the computed tiles (large-tile kernel: 256 x 256 tiles, checked when kp > 192)
+    computed_ops, skipped_share = int8_ops, 0.0
+    if bad > 0.0 and emu:
+        if i8_kernel != "i8_large_kernel":
+            computed_ops = None   # tile shapes per product are the schedule's choice: not counted here
+        else:
+            computed_ops = 0.0
+            for g in emu:
+                m, n, k = shapes[g][:3]
+                kp = kp_of(k)
+                rf = torch.isfinite(A[g]).all(dim=0).view(-1)   # rows of A (torch (k, m))
+                cf = torch.isfinite(B[g]).all(dim=1).view(-1)   # columns of B (torch (n, k))
+                tr = torch.nn.functional.pad(rf, (0, (-m) % 256)).view(-1, 256).any(dim=1)
+                tc = torch.nn.functional.pad(cf, (0, (-n) % 256)).view(-1, 256).any(dim=1)
+                live = int((tr[:, None] & tc[None, :]).sum().item()) if kp > 192 else tr.numel() * tc.numel()
+                computed_ops += (plan_e[g].num_moduli + 1) * 2.0 * m * n * kp * live / (tr.numel() * tc.numel())
+            skipped_share = 1.0 - computed_ops / int8_ops
+    achieved = computed_ops / (i8_ms * 1e-3) / 1e12 if computed_ops and i8_ms > 0 else None
     prep_bytes = sum(8.0 * (shapes[g][0] * shapes[g][2] + shapes[g][1] * shapes[g][2]) +
                      (plan_e[g].num_moduli + 1) * (shapes[g][0] + shapes[g][1]) * kp_of(shapes[g][2]) +
                      16.0 * (shapes[g][0] + shapes[g][1]) for g in emu)
@@ -365,7 +384,8 @@ def main():
                    "execution": "plan/execute (hipGraph), pointers updated per run" if plan_used
                    else "ggemm_grouped_dgemm per run",
                    "num_moduli": [st.moduli_min, st.moduli_max], "repair": "ON"},
-        "int8_mfma_frac_end_to_end": round(int8_ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4),
+        "int8_mfma_frac_end_to_end": None if computed_ops is None else round(
+            computed_ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4),
         "fp64_mfma_frac": round(value / FP64_PEAK_TFLOPS, 4),
         "native_fp64_tflops": None if native_tflops is None else round(native_tflops, 3),
         "emulated_flop_share": round(emu_flops / flops, 4),
@@ -374,9 +394,12 @@ def main():
                      "native": round(st_ms[3], 4)},
         "stage_hbm_gbs": {"prep": round(prep_bytes / (st_ms[0] * 1e-3) / 1e9, 1) if st_ms[0] else None,
                           "reconstruct": round(recon_bytes / (st_ms[2] * 1e-3) / 1e9, 1) if st_ms[2] else None},
-        "roofline": {"bound": "mfma", "kernel": i8_kernel, "achieved": round(achieved, 2),
-                     "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s", "frac": round(achieved / INT8_PEAK_TOPS, 4),
-                     "traffic": measured_traffic(args.workload, i8_kernel)},
+        "roofline": {"bound": "mfma", "kernel": i8_kernel,
+                     "achieved": None if achieved is None else round(achieved, 2),
+                     "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
+                     "frac": None if achieved is None else round(achieved / INT8_PEAK_TOPS, 4),
+                     "traffic": measured_traffic(args.workload, i8_kernel),
+                     "skipped_tile_ops_share": round(skipped_share, 4)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))
