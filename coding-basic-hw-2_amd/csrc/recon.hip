@@ -165,7 +165,7 @@ __device__ __forceinline__ void wave_dots(const oz2_problem& pr, int wr0, int wc
   for (int e = 0; e < 4; ++e) acc[e] = 0.0;
   if (K <= 0) return;
   // the chunk's 8 values per lane come from clamped (always valid) addresses, all loads in flight
-  // at once (no prefetch across chunks: it would cost the kernel its fifth wave per SIMD); values
+  // at once (no prefetch across chunks: it would cost the kernel waves per SIMD); values
   // outside the problem stage as zero
   const int colB = min(wc0 + sk, n - 1);
   const bool inB = wc0 + sk < n;
@@ -669,11 +669,11 @@ __device__ __forceinline__ void compact_dots(const oz2_problem& pr, int r0, int 
   const int t = threadIdx.x;
   const int lr = nR > 1 ? 32 - __clz(nR - 1) : 0;   // nRp = 2^lr >= nR
   const int nq = (1 << lr) + nC;
-  const int kcap = min(kUnion / nq - 2, 6 * kThreads / nq);
+  constexpr int NS = 4;   // staging loads per thread (6 cost the kernel its sixth wave per SIMD)
+  const int kcap = min(kUnion / nq - 2, NS * kThreads / nq);
   const int lg = 31 - __clz(kcap);   // KC = 2^lg <= kcap
   const int KC = 1 << lg, S = KC + 2;
   const int nA = KC << lr, nS = nq * KC;   // staging elements: A rows (padded to nRp), B columns
-  constexpr int NS = 6;   // staging loads per thread (8 would cost the kernel its fifth wave per SIMD)
   double v[NS];
   auto fetch = [&](int kc) {
 #pragma unroll
@@ -808,8 +808,8 @@ __device__ __forceinline__ void sparse_dots(const oz2_problem& pr, int r0, int c
   }
 }
 
-// (launch bounds: five waves per SIMD, which the chains' latency needs)
-__global__ void __launch_bounds__(kThreads, 5) dots_kernel(const oz2_problem* __restrict__ probs,
+// (launch bounds: six waves per SIMD, which the chains' latency needs; seven spill)
+__global__ void __launch_bounds__(kThreads, 6) dots_kernel(const oz2_problem* __restrict__ probs,
                                                         const YDesc* __restrict__ yds, int gne, int gper, int form) {
   __shared__ __attribute__((aligned(16))) double buf[kUnion];
   __shared__ uint64_t fl[64];       // flag words of the tile's 16 blocks (4 per block, column-major blocks)

@@ -1,7 +1,7 @@
 /* oz2_oracle.c -- CPU oracle for the grouped Ozaki-II FP64 GEMM (TEST INFRASTRUCTURE ONLY).
  *
  * Plain C restatement of the reference's behaviour, written from its formulas and operation
- * order; the checker for tests/, smoke() and bench.py's cpu_baseline leg.  See oz2_oracle.h
+ * order; what tests/, smoke() and bench.py's cpu_baseline leg compare against.  See oz2_oracle.h
  * for what pins each part.  Build: oracle/Makefile (gcc, -ffp-contract=off so that only the
  * fma() calls written below fuse, matching the reference's explicit fma()s and the two
  * multiply-adds its device compiler contracts).
