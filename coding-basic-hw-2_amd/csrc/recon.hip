@@ -654,7 +654,7 @@ __device__ __forceinline__ void dense_dots(const oz2_problem& pr, int r0, int c0
 // The chains of the crossings of nR tile rows (rmap) and nC tile columns (cmap), nR nC <= kCompactMax:
 // thread t < nR nC runs the chain of row rmap[t / nC], column cmap[t % nC] and stores it if that
 // entry is flagged.  Per k-chunk of KC (the largest power of two with nRp + nC rows of KC + 2
-// doubles in the LDS union and at most 6 staging loads per thread; nRp = nR rounded up to a power
+// doubles in the LDS union and at most NS staging loads per thread; nRp = nR rounded up to a power
 // of two) the rows of A are staged with consecutive threads on consecutive rows (A is column-major)
 // and the columns of B with consecutive threads on consecutive k, the next chunk's loads in flight
 // while the chains run; a chain reads its row and column two k at a time (16-byte LDS reads; KC + 2
@@ -688,34 +688,42 @@ __device__ __forceinline__ void compact_dots(const oz2_problem& pr, int r0, int 
       }
     }
   };
-  auto put = [&]() {
+  auto put = [&](double* dst) {
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       const int x = t + kThreads * s;
       if (x < nA) {
         const int q = x & ((1 << lr) - 1);
-        if (q < nR) buf[q * S + (x >> lr)] = v[s];
+        if (q < nR) dst[q * S + (x >> lr)] = v[s];
       } else if (x < nS) {
         const int y = x - nA;
-        buf[(nR + (y >> lg)) * S + (y & (KC - 1))] = v[s];
+        dst[(nR + (y >> lg)) * S + (y & (KC - 1))] = v[s];
       }
     }
   };
+  // two chunk buffers when the LDS union holds them at this chunk length: chunk i + 1 is staged
+  // into the other buffer while chunk i's chains run, one barrier per chunk; else one buffer, the
+  // next chunk staged after a barrier
+  const bool two = 2 * nq * S <= kUnion;
+  const int nb = nq * S;   // doubles per chunk buffer
   const bool act = t < nR * nC;
   const int cr = act ? t / nC : 0, cc = act ? t - cr * nC : 0;
-  const double* a_ = buf + cr * S;
-  const double* b_ = buf + (nR + cc) * S;
+  const int ao = cr * S, bo = (nR + cc) * S;
   double acc = 0.0;
   if (K > 0) {
     fetch(0);
-    put();
+    put(buf);
+    if (two && KC < K) fetch(KC);
   }
   lds_sync();
+  int cur = 0;
   for (int kc = 0; kc < K; kc += KC) {
     const int kn = min(KC, K - kc);
     const bool more = kc + KC < K;
-    if (more) fetch(kc + KC);   // in flight while the chains run
+    if (!two && more) fetch(kc + KC);   // in flight while the chains run
     if (act) {
+      const double* a_ = buf + cur * nb + ao;
+      const double* b_ = buf + cur * nb + bo;
       int kk = 0;
 #pragma unroll 2
       for (; kk + 2 <= kn; kk += 2) {
@@ -726,10 +734,19 @@ __device__ __forceinline__ void compact_dots(const oz2_problem& pr, int r0, int 
       }
       if (kk < kn) acc = fma(a_[kk], b_[kk], acc);
     }
-    lds_sync();   // every chain done with this chunk
-    if (more) {
-      put();
-      lds_sync();
+    if (two) {
+      if (more) {
+        put(buf + (cur ^ 1) * nb);   // chunk kc + KC (the other buffer's last readers passed a barrier)
+        if (kc + 2 * KC < K) fetch(kc + 2 * KC);
+      }
+      lds_sync();   // chunk kc's chains done, chunk kc + KC staged
+      cur ^= 1;
+    } else {
+      lds_sync();   // every chain done with this chunk
+      if (more) {
+        put(buf);
+        lds_sync();
+      }
     }
   }
   if (act) {
