@@ -201,16 +201,23 @@ def test_plan_replays_alternate_nonfinite_and_finite_data():
     (ggemm_plan_update_pointers between the runs), repair ON.  Prep marks problems with non-finite
     rows / columns and the reconstruct marks problems with flagged entries in the plan's device
     descriptors; a replay on finite data after one on non-finite data sees those marks still set
-    and must take the general paths, so every run is compared with the oracle bit for bit."""
+    and must take the general paths, so every run is compared with the oracle bit for bit.  In X
+    every A row of problem 0 and every B column of problem 2 holds a non-finite value, so the INT8
+    GEMM skips their tiles there; on Y, with the marks still set, it must compute them."""
     shapes = [(200, 150, 300)] * 2 + [(64, 96, 1200), (130, 70, 40)]
     X = Case(shapes, 81, phi=2.0, alpha=1.5, beta=0.5)
     Y = Case(shapes, 82, phi=1.0, alpha=1.5, beta=0.5)
     rng = np.random.default_rng(83)
+    bad = [np.nan, np.inf, -np.inf]
     for hp in X.hp:
         for arr, rows, cols, ld in ((hp.A, hp.m, hp.k, hp.lda), (hp.B, hp.k, hp.n, hp.ldb)):
             nbad = max(1, rows * cols // 1500)
-            arr[rng.integers(0, rows, nbad) + rng.integers(0, cols, nbad) * ld] = rng.choice(
-                [np.nan, np.inf, -np.inf], nbad)
+            arr[rng.integers(0, rows, nbad) + rng.integers(0, cols, nbad) * ld] = rng.choice(bad, nbad)
+    h0, h2 = X.hp[0], X.hp[2]
+    for i in range(h0.m):
+        h0.A[i + rng.integers(0, h0.k) * h0.lda] = bad[i % 3]
+    for j in range(h2.n):
+        h2.B[rng.integers(0, h2.k) + j * h2.ldb] = bad[j % 3]
     X.alloc()
     cfg = G.Config(0, 1e-15, 0, G.REPAIR_ON)
     rc, plan_o = oracle_plan(X, cfg, G.PATH_EMU_GROUPED)
