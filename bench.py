@@ -372,7 +372,7 @@ def main():
     # ---- CPU baseline: the host FP64 GEMM (OpenMP) on a bounded sample of the same problems
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(shapes, A, B, budget_s=15.0)
+        cpu = cpu_baseline(shapes, A, B, C0, budget_s=15.0)
 
     value = flops / (ms * 1e-3) / 1e12
     out = {
@@ -503,21 +503,22 @@ def validate_counters(G, torch, shapes, C0, Cm, keep, path, cfg, problems, min_k
                       "kernel_launches": stv.kernel_launches, "moduli": [stv.moduli_min, stv.moduli_max]}}
 
 
-def cpu_baseline(shapes, A, B, budget_s):
+def cpu_baseline(shapes, A, B, C0, budget_s):
     """The host blocked FP64 GEMM (oracle/oz2_dgemm.c, OpenMP) on as many of the workload's problems
-    as fit in about budget_s seconds (at least one), in the workload's order."""
+    as fit in about budget_s seconds (at least one), in the workload's order, each with its own
+    alpha, beta and C0 (C0: the workload's initial C per problem, or None when every beta is 0)."""
     sys.path.insert(0, str(REPO / "tests"))
     import oracle_lib as O
     ora = O.oracle()
     model, mask, ncpu, naff = host_cpu()
     threads = int(os.environ.get("OMP_NUM_THREADS", naff))
     done, t_cpu, fl = 0, 0.0, 0.0
-    for g, (m, n, k, a, *_r) in enumerate(shapes):
+    for g, (m, n, k, a, b, *_r) in enumerate(shapes):
         ha = A[g].cpu().numpy().reshape(-1)
         hb = B[g].cpu().numpy().reshape(-1)
-        hc = np.zeros(m * n)
+        hc = np.zeros(m * n) if C0 is None or b == 0.0 else C0[g].cpu().numpy().reshape(-1).copy()
         t1 = time.perf_counter()
-        ora.oz2o_dgemm(m, n, k, 1.0, ha, m, hb, k, 0.0, hc, m)
+        ora.oz2o_dgemm(m, n, k, a, ha, m, hb, k, b, hc, m)
         t_cpu += time.perf_counter() - t1
         fl += 2.0 * m * n * k
         done += 1

@@ -120,6 +120,7 @@ __host__ __device__ inline int i8_tile_n(int cfg) { return cfg == 0 ? 128 : (cfg
 enum : uint32_t { kEpiResidue = 1u, kEpiBlocked = 2u, kEpiPacked = 4u, kEpiAccBias = 8u };
 constexpr int kAccBiasMaxKp = 32768;   // |C| <= 128^2 kp <= 2^29
 constexpr int kPackedMaxKp = 4096;   // production problems whose Kp is at most this use packing
+constexpr int kKpMaxPacked = 1 << 30;   // packed_kp of a call that packs every problem
 __host__ __device__ inline size_t packed_offset(int row, int k, int rows, int kp) {
   const int b = k >> 6;
   const int rb = b == (kp >> 6) ? 32 : 64;
@@ -155,6 +156,12 @@ enum { kI8General = 0, kI8Large = 1, kI8Persistent = 2 };
 enum { kLargeNever = 0, kLargeAuto = 1, kLargeForce = 2 };
 int i8_build_schedule(const i8_problem* h, int num, void* h_ws, size_t ws_bytes, i8_sched_info* info,
                       int num_cus, int large = kLargeNever, int* kernel = nullptr, bool persistent = false);
+// The tile configuration i8_build_schedule gives an m x n product with tile_cfg < 0 (before the
+// group-level shrink).
+int i8_auto_tile_cfg(int m, int n);
+// Sizes the schedule builder's host scratch for `entries` (problem, plane) products, so that
+// i8_build_schedule allocates nothing for calls of at most that many (handle / plan creation).
+void i8_reserve_host(size_t entries);
 // GGEMM_I8_SCHED=persistent in the environment (read at each call): the kernel-level INT8 API
 // (i8_grouped_gemm_*) builds for and runs the persistent kernels
 bool i8_env_persistent();
@@ -281,6 +288,7 @@ struct ggemm_handle_s {
                        // only, the kernel-level layouts (testing)
   int f64_tile;        // GGEMM_F64_TILE at create: 0 automatic, 64 or 128 forces the native GEMM's tile edge
   int packed_max_kp;   // GGEMM_PACKED_MAX_KP at create: calls whose largest Kp is at most this use packed residues
+  int packed_env;      // GGEMM_PACKED_MAX_KP was given: its threshold holds for every call
   int i8_persistent;   // GGEMM_I8_SCHED=persistent at create: the persistent work-stealing INT8 kernels
   int safety_chains;   // GGEMM_SAFETY_CHAINS=1 at create: safety-fallback entries always run their fma
                        // chains instead of being decided from prep's non-finite summaries (testing)

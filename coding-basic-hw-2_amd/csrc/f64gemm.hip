@@ -193,21 +193,25 @@ int f64_build_schedule(const F64Problem* h, int num, void* h_ws, size_t ws_bytes
       }
     if (t128 >= 1024 && 4 * t128 * 8 <= a64 * 9) tile = 128;
   }
+  // problems with outputs, longest k first (ties by index: the order a stable sort keeps), sorted
+  // in place in the image's entry array -- no host scratch
   int* img = static_cast<int*>(h_ws);
-  std::vector<std::pair<double, int>> order;
-  order.reserve(num);
-  for (int i = 0; i < num; ++i)
-    if (h[i].m > 0 && h[i].n > 0) order.push_back({(double)std::max(h[i].k, 1), i});
-  std::stable_sort(order.begin(), order.end(), [](auto& a, auto& b) { return a.first > b.first; });
-  const size_t ne = order.size();
+  size_t ne = 0;
+  for (int i = 0; i < num; ++i) ne += h[i].m > 0 && h[i].n > 0;
   int* prefix = img + kSchedHdr;
   int* entry = prefix + ne + 1;
+  for (int i = 0, j = 0; i < num; ++i)
+    if (h[i].m > 0 && h[i].n > 0) entry[j++] = i;
+  std::sort(entry, entry + ne, [h](int a, int b) {
+    const int ka = std::max(h[a].k, 1), kb = std::max(h[b].k, 1);
+    return ka != kb ? ka > kb : a < b;
+  });
   long long tot = 0;
   for (size_t j = 0; j < ne; ++j) {
-    const F64Problem& p = h[order[j].second];
+    const F64Problem& p = h[entry[j]];
     prefix[j] = (int)tot;
     tot += tiles_of(p, tile);
-    entry[j] = order[j].second << 2;
+    entry[j] <<= 2;
   }
   prefix[ne] = (int)tot;
   if (tot >= kF64Tile128) return 5;

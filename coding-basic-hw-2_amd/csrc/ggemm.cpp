@@ -142,6 +142,22 @@ int large_mode(ggemm_handle_t h, const GroupedCall& c) {
   return c.packed ? kLargeNever : kLargeAuto;
 }
 
+// Whether i8_build_schedule can give this call the 256 x 256 kernel under kLargeAuto: every
+// (problem, plane) product on automatic 256 x 128 tiles, kept by the group-level fill rule (at
+// least two such tiles per compute unit), and a 256 x 256 tile for every compute unit.
+bool large_auto_fits(ggemm_handle_t h, const ggemm_problem_t* probs, const int* emu_idx,
+                     const ggemm_plan_entry_t* plan, int ne) {
+  long long t0 = 0, t256 = 0;
+  for (int j = 0; j < ne; ++j) {
+    const ggemm_problem_t& p = probs[emu_idx[j]];
+    if (i8_auto_tile_cfg(p.m, p.n) != 0) return false;
+    const long long planes = plan[emu_idx[j]].num_moduli + 1;
+    t0 += planes * ((p.m + 255) / 256) * ((p.n + 127) / 128);
+    t256 += planes * ((p.m + 255) / 256) * ((p.n + 255) / 256);
+  }
+  return ne > 0 && t0 >= 2LL * h->num_cus && t256 >= h->num_cus;
+}
+
 int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const ggemm_plan_entry_t* plan,
                   int* emu_idx, int* nat_idx, char* hb, const char* db, size_t cap, GroupedCall* out,
                   ggemm_stats_t* st, const reuse_plan* rp) {
@@ -240,12 +256,18 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
   const bool nfsum = c.blocked && !rp && !h->safety_chains && (size_t)nmax * SYb + SLb + SFb + SNF <= h->C32_bytes;
   // Packed residue planes make every 64-byte k-stage of a tile's rows contiguous, which the INT8
   // GEMM's operand stream prefers at moderate k (measured: 1024^3 products 14 % faster together
-  // with the blocked digits); at k = 16384 the row-major planes stream better (5 % slower packed).
-  // The choice is per problem (Kp <= packed_kp), so the long-k problems of a ragged group do not
-  // put its short ones on row-major planes.
+  // with the blocked digits); at k = 16384 the 256 x 256 kernel streams row-major planes better
+  // (5 % slower packed).  The choice is per problem (Kp <= packed_kp), so the long-k problems of a
+  // ragged group do not put its short ones on row-major planes; and when the call cannot take the
+  // 256 x 256 kernel at all, every problem is packed -- the general kernel streams packed planes
+  // better at long k too (ragged group G = 128, k up to 8192: GEMM 2.27 -> 2.13 ms, prep 1.87 ->
+  // 1.76 ms, same box).
   int max_kp = 0;
   for (int j = 0; j < c.ne; ++j) max_kp = std::max(max_kp, kp_of(probs[emu_idx[j]].k));
   c.packed_kp = h->digits_colmajor ? 0 : h->packed_max_kp;
+  if (!h->digits_colmajor && !h->packed_env && max_kp > c.packed_kp && h->i8_mode != 2 &&
+      (h->i8_mode == 1 || !large_auto_fits(h, probs, emu_idx, plan, c.ne)))
+    c.packed_kp = kKpMaxPacked;
   c.packed = max_kp <= c.packed_kp;
   c.dot_form = h->dot_form;
   if (c.blocked) SY = SYb;
@@ -362,7 +384,8 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
     int* po = reinterpret_cast<int*>(hb + c.L.off_po);
     for (int i = 0; i < np; ++i) po[i] = i;
     auto vol = [&](int i) { return ((long long)pd[i].m + pd[i].n) * pd[i].kp; };
-    std::stable_sort(po, po + np, [&](int a, int b) { return vol(a) > vol(b); });
+    // ties by index (the order a stable sort keeps; std::sort takes no temporary buffer)
+    std::sort(po, po + np, [&](int a, int b) { return vol(a) != vol(b) ? vol(a) > vol(b) : a < b; });
     // compact grid: each problem's first block, in dispatch order (problems prep skips get none)
     int* pof = po + np;
     long long tot = 0;
@@ -759,6 +782,9 @@ extern "C" int ggemm_create_ex(ggemm_handle_t* out, int max_problems, size_t max
   h->nat_idx = new (std::nothrow) int[P];
   h->loop_info = new (std::nothrow) i8_sched_info[P * M];
   if (!h->plan || !h->plan_memo || !h->emu_idx || !h->nat_idx || !h->loop_info) FAIL(GGEMM_ERR_ALLOC);
+  // the INT8 schedule builder's host scratch for P (problem, plane) products of every call
+  // (src/ggemm.cu:287): calls through this handle allocate no host memory
+  i8_reserve_host(P * M);
   // operand reuse: host arena and offset scratch (nothing is allocated inside calls)
   if (reuse_arena_create(max_problems, &h->reuse) != REUSE_OK) FAIL(h->reuse ? GGEMM_ERR_INVALID : GGEMM_ERR_ALLOC);
   h->reuse_nmod = new (std::nothrow) int[P];
@@ -781,6 +807,7 @@ extern "C" int ggemm_create_ex(ggemm_handle_t* out, int max_problems, size_t max
   h->i8_persistent = (esc && !std::strcmp(esc, "persistent")) ? 1 : 0;
   const char* epk = std::getenv("GGEMM_PACKED_MAX_KP");
   h->packed_max_kp = epk ? std::max(0, std::atoi(epk)) : kPackedMaxKp;
+  h->packed_env = epk ? 1 : 0;
   const char* esf = std::getenv("GGEMM_SAFETY_CHAINS");
   h->safety_chains = (esf && std::atoi(esf) == 1) ? 1 : 0;
   const char* edf = std::getenv("GGEMM_DOT_FORM");

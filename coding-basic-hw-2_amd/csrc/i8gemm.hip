@@ -42,6 +42,7 @@
 // The production pipeline also stores in the blocked layout: each 16 x 16 MFMA result block is one
 // contiguous 256-byte (digits) or 1 KB (int32) store instead of 16 column pieces.
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -808,9 +809,59 @@ struct Ent {
   double cost;
   int tiles, prob, cfg;
 };
+// Host scratch of the schedule builder (entries, their order, the XCD queue of each entry), sized
+// by i8_grouped_gemm_reserve at handle / plan creation so that building a schedule allocates
+// nothing; a larger call still works and grows it, which i8_grouped_gemm_host_allocs counts
+// (src/int8_grouped_gemm.cu:541-589).  The kernel-level i8_grouped_gemm_ex keeps its schedule
+// image in a buffer of its own, reserved and counted the same way.
 std::mutex g_mu;
-std::vector<Ent> g_ents;
-std::vector<int> g_order;
+Ent* g_ents = nullptr;
+int* g_order = nullptr;
+int* g_xq = nullptr;
+size_t g_cap = 0;
+std::mutex g_img_mu;
+int* g_img = nullptr;
+size_t g_img_cap = 0;
+std::atomic<long long> g_host_allocs{0};
+
+// capacity for n schedule images (g_img_mu held)
+bool ensure_img_capacity(size_t n) {
+  const size_t img = sched_bytes((int)std::min<size_t>(std::max<size_t>(n, 1), 0x3fffffff)) / sizeof(int) + 1;
+  if (img > g_img_cap) {
+    int* q = new (std::nothrow) int[img];
+    if (!q) return false;
+    delete[] g_img;
+    g_img = q;
+    g_img_cap = img;
+    ++g_host_allocs;
+  }
+  return true;
+}
+
+// capacity for n schedule entries (g_mu held); false when the host is out of memory
+bool ensure_capacity(size_t n) {
+  n = std::max<size_t>(n, 1);
+  if (n > g_cap) {
+    Ent* e = new (std::nothrow) Ent[n];
+    int* o = new (std::nothrow) int[n];
+    int* x = new (std::nothrow) int[n];
+    if (!e || !o || !x) {
+      delete[] e;
+      delete[] o;
+      delete[] x;
+      return false;
+    }
+    delete[] g_ents;
+    delete[] g_order;
+    delete[] g_xq;
+    g_ents = e;
+    g_order = o;
+    g_xq = x;
+    g_cap = n;
+    ++g_host_allocs;
+  }
+  return true;
+}
 
 bool valid_problem(const i8_problem& p) {
   if (p.m < 0 || p.n < 0 || p.kp < 0 || (p.kp % 32) != 0 || p.kp > OZ2_MAX_K) return false;
@@ -837,6 +888,8 @@ int auto_cfg(int m, int n) {
 
 }  // namespace
 
+int i8_auto_tile_cfg(int m, int n) { return auto_cfg(m, n); }
+
 bool i8_env_persistent() {
   const char* e = std::getenv("GGEMM_I8_SCHED");
   return e && !std::strcmp(e, "persistent");
@@ -848,55 +901,59 @@ int i8_build_schedule(const i8_problem* h, int num, void* h_ws, size_t ws_bytes,
   if (ws_bytes < sched_bytes(num)) return 2;
   if (kernel) *kernel = kI8General;
   std::lock_guard<std::mutex> lk(g_mu);
-  std::vector<Ent>& ents = g_ents;
-  ents.clear();
+  if (!ensure_capacity((size_t)num)) return 6;
+  Ent* const ents = g_ents;
+  size_t ne = 0;
   for (int i = 0; i < num; ++i) {
     if (!valid_problem(h[i])) return 3;
     if (h[i].m == 0 || h[i].n == 0 || h[i].kp == 0) continue;
     int c = h[i].tile_cfg;
     if (c < 0) c = auto_cfg(h[i].m, h[i].n);
     if (c >= kI8NumCfg) c = kI8NumCfg - 1;
-    ents.push_back({(double)i8_tile_m(c) * i8_tile_n(c) * (double)(h[i].kp + 128), tiles_of(c, h[i].m, h[i].n), i, c});
+    ents[ne++] = {(double)i8_tile_m(c) * i8_tile_n(c) * (double)(h[i].kp + 128), tiles_of(c, h[i].m, h[i].n), i, c};
   }
-  bool all_auto = !ents.empty();
-  for (auto& e : ents) all_auto = all_auto && h[e.prob].tile_cfg < 0;
+  Ent* const ents_end = ents + ne;
+  bool all_auto = ne > 0;
+  for (const Ent* e = ents; e != ents_end; ++e) all_auto = all_auto && h[e->prob].tile_cfg < 0;
   const bool force_large = large == kLargeForce && all_auto;
   // group-level fill: fewer tiles than workgroup slots (2 per compute unit) -> shrink automatic
   // tiles one step
   for (int pass = 0; pass < 2 && !force_large; ++pass) {
     long long t = 0;
-    for (auto& e : ents) t += e.tiles;
+    for (const Ent* e = ents; e != ents_end; ++e) t += e->tiles;
     if (t >= 2LL * num_cus) break;
-    for (auto& e : ents)
-      if (e.cfg < kI8NumCfg - 1 && h[e.prob].tile_cfg < 0) {
-        ++e.cfg;
-        e.tiles = tiles_of(e.cfg, h[e.prob].m, h[e.prob].n);
-        e.cost = (double)i8_tile_m(e.cfg) * i8_tile_n(e.cfg) * (double)(h[e.prob].kp + 128);
+    for (Ent* e = ents; e != ents_end; ++e)
+      if (e->cfg < kI8NumCfg - 1 && h[e->prob].tile_cfg < 0) {
+        ++e->cfg;
+        e->tiles = tiles_of(e->cfg, h[e->prob].m, h[e->prob].n);
+        e->cost = (double)i8_tile_m(e->cfg) * i8_tile_n(e->cfg) * (double)(h[e->prob].kp + 128);
       }
   }
   // large-tile kernel: every product on automatic large tiles, and enough 256 x 256 tiles to give
   // every compute unit one
-  if (large != kLargeNever && !ents.empty()) {
+  if (large != kLargeNever && ne > 0) {
     bool all = true;
     long long t = 0;
-    for (auto& e : ents) {
-      all = all && e.cfg == 0 && h[e.prob].tile_cfg < 0;
-      t += (long long)((h[e.prob].m + 255) / 256) * ((h[e.prob].n + 255) / 256);
+    for (const Ent* e = ents; e != ents_end; ++e) {
+      all = all && e->cfg == 0 && h[e->prob].tile_cfg < 0;
+      t += (long long)((h[e->prob].m + 255) / 256) * ((h[e->prob].n + 255) / 256);
     }
     if (force_large || (all && t >= num_cus)) {
-      for (auto& e : ents) {
-        e.cfg = 0;
-        e.tiles = ((h[e.prob].m + 255) / 256) * ((h[e.prob].n + 255) / 256);
-        e.cost = 256.0 * 256.0 * (double)(h[e.prob].kp + 128);
+      for (Ent* e = ents; e != ents_end; ++e) {
+        e->cfg = 0;
+        e->tiles = ((h[e->prob].m + 255) / 256) * ((h[e->prob].n + 255) / 256);
+        e->cost = 256.0 * 256.0 * (double)(h[e->prob].kp + 128);
       }
       if (kernel) *kernel = kI8Large;
     }
   }
   if (kernel && persistent) *kernel |= kI8Persistent;
-  // longest-processing-time order (heaviest tiles first)
-  std::stable_sort(ents.begin(), ents.end(), [](const Ent& a, const Ent& b) {
+  // longest-processing-time order (heaviest tiles first; ties by problem index, i.e. the order a
+  // stable sort keeps -- std::sort takes no temporary buffer)
+  std::sort(ents, ents_end, [](const Ent& a, const Ent& b) {
     if (a.cost != b.cost) return a.cost > b.cost;
-    return a.tiles > b.tiles;
+    if (a.tiles != b.tiles) return a.tiles > b.tiles;
+    return a.prob < b.prob;
   });
   // Queues of the persistent kernels: chunks of c consecutive tiles of the LPT table dealt
   // round-robin to the XCDs (c = 32, GGEMM_I8_CHUNK=c overrides; same-box GEMM times at c = 32 vs
@@ -909,12 +966,10 @@ int i8_build_schedule(const i8_problem* h, int num, void* h_ws, size_t ws_bytes,
     return e ? std::max(0, std::atoi(e)) : kChunk;
   }();
   const int chunk = persistent ? env_chunk : 1;
-  const size_t ne = ents.size();
-  std::vector<int>& order = g_order;
-  order.resize(ne);
+  int* const order = g_order;
+  int* const xq = g_xq;
   double load[kXcds] = {};
   int count[kXcds] = {};
-  std::vector<int> xq(ne);
   for (size_t j = 0; j < ne; ++j) {
     int best = 0;
     for (int x = 1; x < kXcds && chunk == 0; ++x)
@@ -969,12 +1024,12 @@ I8Epi i8_epi_residue(uint32_t p, int kp) {
 namespace {
 // the kernels' dynamic LDS exceeds the default limit: raise it once per device
 bool lds_attrs_set() {
+  constexpr int kMaxDevices = 64;
   static std::mutex mu;
-  static std::vector<int> done;
+  static bool done[kMaxDevices];
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return false;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
   std::lock_guard<std::mutex> lk(mu);
-  if ((int)done.size() <= dev) done.resize(dev + 1, 0);
   if (!done[dev]) {
     if (hipFuncSetAttribute((const void*)i8_grouped_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kSmem) !=
             hipSuccess ||
@@ -985,11 +1040,20 @@ bool lds_attrs_set() {
         hipFuncSetAttribute((const void*)i8_large_persistent_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                             kSmemL) != hipSuccess)
       return false;
-    done[dev] = 1;
+    done[dev] = true;
   }
   return true;
 }
 }  // namespace
+
+void i8_reserve_host(size_t entries) {
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    ensure_capacity(entries);
+  }
+  std::lock_guard<std::mutex> lk(g_img_mu);
+  ensure_img_capacity(entries);
+}
 
 int i8_launch(const i8_problem* d_probs, const I8Epi* d_epi, const void* d_sched, const i8_sched_info* info,
               hipStream_t s, int kernel) {
@@ -1033,6 +1097,12 @@ extern "C" size_t i8_grouped_gemm_sched_ws_bytes(int max_problems, size_t) {
   return sched_bytes(max_problems < 0 ? 0 : max_problems);
 }
 
+extern "C" void i8_grouped_gemm_reserve(int max_problems, size_t) {
+  i8_reserve_host(max_problems > 0 ? (size_t)max_problems : 1);
+}
+
+extern "C" long long i8_grouped_gemm_host_allocs() { return g_host_allocs.load(); }
+
 extern "C" int i8_grouped_gemm_build_schedule(const i8_problem* h_probs, int num, void* h_ws, size_t ws_bytes,
                                               i8_sched_info* info) {
   DevCtx* c = dev_ctx();
@@ -1052,12 +1122,16 @@ extern "C" int i8_grouped_gemm_ex(const i8_problem* d_probs, int num, const i8_p
   if (!d_sched_ws) return 1;
   const size_t need = sched_bytes(num);
   if (need > sched_ws_bytes) return 2;
-  std::vector<int> img(need / sizeof(int) + 1);
+  // the image goes through the reserved host buffer (one call at a time: the copy below is waited
+  // for before the buffer is released)
+  std::lock_guard<std::mutex> lk(g_img_mu);
+  if (!ensure_img_capacity((size_t)num)) return 6;
+  int* const img = g_img;
   i8_sched_info info;
-  int rc = i8_grouped_gemm_build_schedule(h_probs, num, img.data(), need, &info);
+  int rc = i8_grouped_gemm_build_schedule(h_probs, num, img, need, &info);
   if (rc) return rc;
   if (info.num_launches == 0) return 0;
-  if (hipMemcpyAsync(d_sched_ws, img.data(), info.bytes_used, hipMemcpyHostToDevice, s) != hipSuccess) return 7;
+  if (hipMemcpyAsync(d_sched_ws, img, info.bytes_used, hipMemcpyHostToDevice, s) != hipSuccess) return 7;
   // the pageable source must stay valid until the copy has consumed it
   if (hipStreamSynchronize(s) != hipSuccess) return 7;
   rc = i8_launch(d_probs, nullptr, d_sched_ws, &info, s, i8_env_persistent() ? kI8Persistent : kI8General);

@@ -1,6 +1,8 @@
 // noalloc.hip -- ggemm_grouped_dgemm_noalloc: the grouped emulated DGEMM without a handle and without
-// any allocation, for callers that cannot allocate device memory (code under stream capture, tight
-// serving loops, harnesses that forbid hipMalloc).  It has no counterpart in the reference.
+// any allocation, for callers that cannot allocate device memory (tight serving loops, harnesses
+// that forbid hipMalloc).  It has no counterpart in the reference.  It is not capturable: the call
+// waits for its descriptor copy (a stream synchronisation), so on a stream that is being captured
+// it returns GGEMM_ERR_INVALID before any HIP call that would invalidate the capture.
 //
 // Every device buffer the pipeline needs beyond the caller's A, B and C -- residue planes, CRT digit
 // and abs-plane products, row / column shift words, the descriptor blob and tile schedules -- lives
@@ -8,14 +10,18 @@
 // the life of the process.  It is carved exactly like the workspace of a handle created with
 // ggemm_create(GGEMM_NOALLOC_MAX_PROBLEMS, GGEMM_NOALLOC_MAX_ELEMS x 3): the same kernels run on the
 // same layouts, so the bits equal ggemm_grouped_dgemm's.  Host-side scratch (plan entries, index
-// lists, the descriptor image) is static too.
+// lists, the descriptor image, the INT8 and FP64 tile-schedule builders' work arrays) is static or
+// sized once at set-up, so a call allocates no host memory either.
 //
 // Set-up, once per device on the first call with that device current: hipGetSymbolAddress of
 // `scratch` (its device address on this GPU; the array's name in host code is only a host-side
 // stand-in), the device model and the resident CRT tables (device globals, filled by a copy).
 // Every call on a GPU shares that GPU's scratch and it keeps the last call's contents; nothing in
-// it needs to start at zero (every byte a call reads it has written first in the same call, the
-// digit and residue padding included).  Calls are serialised on the host by a mutex; the
+// it needs to start at zero: every byte whose value reaches an output the call has written first
+// (the digit and residue padding included).  The residue planes of rows / columns that hold a NaN
+// or an Inf are not written; the INT8 GEMM may read whatever bytes an earlier call left there, but
+// only entries that take the safety fallback (which reads neither digits nor products) consume
+// those sums.  Calls are serialised on the host by a mutex; the
 // descriptor image is copied from static host memory and the call waits for that copy (and so for
 // earlier work on the stream) before it enqueues its kernels.  Calls that overlap on one GPU from
 // different streams race on the scratch.
@@ -45,6 +51,7 @@ int g_memo[2 * kMaxProblems];
 int g_emu_idx[kMaxProblems], g_nat_idx[kMaxProblems];
 alignas(256) char g_blob[kHostBlobBytes];
 bool g_limit_reported = false;
+bool g_capture_reported = false;
 
 // Carves this device's scratch into the handle-shaped workspace (returns a GGEMM_ERR_* code).
 int setup(int dev) {
@@ -84,6 +91,7 @@ int setup(int dev) {
   h->plan_memo_cap = sizeof g_memo / sizeof g_memo[0];
   h->emu_idx = g_emu_idx;
   h->nat_idx = g_nat_idx;
+  i8_reserve_host((size_t)kMaxProblems * kMaxPlanes);   // schedule builder's host scratch, once
   const char* e = std::getenv("GGEMM_STATS_REPAIR");
   h->stats_repair = (e && std::atoi(e) == 1) ? 1 : 0;
   return GGEMM_OK;
@@ -119,7 +127,19 @@ extern "C" int ggemm_grouped_dgemm_noalloc(ggemm_path_t path, const ggemm_config
   if (repair < 0) return GGEMM_ERR_INVALID;
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return GGEMM_ERR_CUDA;
+  // the call synchronises its stream (descriptor copy, counters): refuse a capturing stream before
+  // any call that a capture forbids, so the caller's capture stays intact
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cap) != hipSuccess) return GGEMM_ERR_CUDA;
   std::lock_guard<std::mutex> lk(g_mu);
+  if (cap != hipStreamCaptureStatusNone) {
+    if (!g_capture_reported) {
+      g_capture_reported = true;
+      std::fprintf(stderr, "[ggemm] ggemm_grouped_dgemm_noalloc: the stream is being captured; this entry point "
+                           "synchronises its stream and cannot be captured (use ggemm_make_plan)\n");
+    }
+    return GGEMM_ERR_INVALID;
+  }
   if (!g_ready[dev]) {
     const int r = setup(dev);
     if (r) return r;

@@ -129,6 +129,8 @@ SIGNATURES = [
     ("oz2_read_counters", C.c_int, [C.POINTER(Oz2Counters), C.c_int, _P]),
     ("oz2_debug_force_prep_split", None, [C.c_int]),
     ("i8_grouped_gemm_sched_ws_bytes", C.c_size_t, [C.c_int, C.c_size_t]),
+    ("i8_grouped_gemm_reserve", None, [C.c_int, C.c_size_t]),
+    ("i8_grouped_gemm_host_allocs", C.c_longlong, []),
     ("i8_grouped_gemm_build_schedule", C.c_int, [C.POINTER(I8Problem), C.c_int, _P, C.c_size_t,
                                                  C.POINTER(I8SchedInfo)]),
     ("i8_grouped_gemm_launch", C.c_int, [_P, C.c_int, _P, C.POINTER(I8SchedInfo), _P]),

@@ -31,7 +31,8 @@ typedef enum {
   GGEMM_PATH_NATIVE_LOOP = 0,        /* native FP64 (own FP64-MFMA DGEMM), one launch per problem */
   GGEMM_PATH_NATIVE_GROUPED = 1,     /* native FP64, one grouped launch */
   GGEMM_PATH_EMU_LOOP = 2,           /* per problem: prep, one INT8 GEMM per plane, reconstruct */
-  GGEMM_PATH_EMU_GROUPED = 3,        /* fused grouped pipeline: 3 launches for the whole group */
+  GGEMM_PATH_EMU_GROUPED = 3,        /* fused grouped pipeline: 4 launches for the whole group
+                                        (prep, INT8 GEMM, reconstruct, FP64 dot-product pass) */
   GGEMM_PATH_AUTO = 4,               /* EMU_GROUPED + planner (adaptive N, cost-based fallback) */
   GGEMM_PATH_EMU_GROUPED_REUSE = 5,  /* EMU_GROUPED + operand reuse */
   GGEMM_PATH_EMU_LOOP_BATCHED = 6    /* per problem: prep, one INT8 GEMM over its planes, reconstruct */
@@ -105,16 +106,18 @@ int ggemm_grouped_dgemm(ggemm_handle_t h, ggemm_path_t path, const ggemm_config_
                         const ggemm_problem_t* problems, int num_problems, ggemm_stats_t* stats);
 
 /* No counterpart in the reference.  ggemm_grouped_dgemm without a handle and without allocating
- * anything, for callers that cannot allocate device memory (code under stream capture, tight serving
- * loops, harnesses that forbid hipMalloc).  Same kernels, layouts and results (bit for bit) as a call
+ * anything (device or host memory), for callers that cannot allocate (tight serving loops, harnesses
+ * that forbid hipMalloc).  Same kernels, layouts and results (bit for bit) as a call
  * through a handle created with ggemm_create(GGEMM_NOALLOC_MAX_PROBLEMS, GGEMM_NOALLOC_MAX_ELEMS x 3):
  * the workspace is a static device array of GGEMM_NOALLOC_SCRATCH_BYTES that each GPU the library
  * runs on holds until the process ends.  Paths GGEMM_PATH_EMU_GROUPED and GGEMM_PATH_AUTO only
  * (others: GGEMM_ERR_INVALID).  Limits: at most GGEMM_NOALLOC_MAX_PROBLEMS problems
  * (GGEMM_ERR_INVALID) and sum m*k, sum k*n, sum m*n each at most GGEMM_NOALLOC_MAX_ELEMS, residues
  * counted at Kp = round_up(k, 32) (GGEMM_ERR_WORKSPACE); either error prints one line on stderr.
- * Work runs on `stream`; the call returns after its descriptor copy has landed, i.e. after earlier
- * work on the stream.  Every call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * Work runs on `stream`; the call synchronises the stream (it returns after its descriptor copy has
+ * landed, i.e. after earlier work on the stream), so it cannot be captured: on a stream that is being
+ * captured it returns GGEMM_ERR_INVALID (one stderr line) and leaves the capture intact; capture
+ * ggemm_execute_plan instead.  Every call on one GPU shares that GPU's array: calls that overlap on one GPU
  * from different streams race.  Device counters and GGEMM_STATS_REPAIR as for ggemm_grouped_dgemm. */
 #define GGEMM_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
 #define GGEMM_NOALLOC_MAX_PROBLEMS 64

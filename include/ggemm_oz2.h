@@ -95,6 +95,12 @@ int i8_grouped_gemm_build_schedule(const i8_problem* h_probs, int num, void* h_w
 /* src/int8_grouped_gemm.h:82-83: launch only (info->num_launches kernels). */
 int i8_grouped_gemm_launch(const i8_problem* d_probs, int num, const void* d_sched_ws,
                            const i8_sched_info* info, hipStream_t s);
+/* src/int8_grouped_gemm.h:46: sizes the schedule builder's host scratch for max_problems
+ * (problem, plane) products, so that building a schedule of at most that many allocates nothing
+ * (ggemm_create_ex reserves max_problems x 21).  Larger calls still work and grow it. */
+void i8_grouped_gemm_reserve(int max_problems, size_t max_tiles);
+/* src/int8_grouped_gemm.h:48: growths of that host scratch so far (constant after a reserve). */
+long long i8_grouped_gemm_host_allocs(void);
 /* src/int8_grouped_gemm.h:72-73: build schedule + H2D + launch. */
 int i8_grouped_gemm_ex(const i8_problem* d_probs, int num, const i8_problem* h_probs_for_sched,
                        void* d_sched_ws, size_t sched_ws_bytes, hipStream_t s, int* num_launches);

@@ -411,15 +411,26 @@ void oz2o_prep_cols(int n, int k, int N, const double* B, int ldb, int8_t* B8, i
 }
 
 /* ------------------------------------------------------------------------------ int GEMM */
-/* tests/test_i8_grouped.cu:89-96 (int64 brute force); the range check is the kp <= 131040 bound. */
+/* tests/test_i8_grouped.cu:89-96 (int64 brute force); the range check is the kp <= 131040 bound.
+ * The exact dot products come from oz2_i8dot.c (vectorised; four columns of B per pass over a row
+ * of A). */
 int oz2o_i8_gemm(int m, int n, int kp, const int8_t* A8, const int8_t* B8, int32_t* C32) {
   int bad = 0;
-  for (int j = 0; j < n; ++j)
+  int j = 0;
+  for (; j + 4 <= n; j += 4) {
+    const int8_t* b = B8 + (size_t)j * kp;
     for (int i = 0; i < m; ++i) {
-      const int8_t* a = A8 + (size_t)i * kp;
-      const int8_t* b = B8 + (size_t)j * kp;
-      int64_t acc = 0;
-      for (int q = 0; q < kp; ++q) acc += (int32_t)a[q] * (int32_t)b[q];
+      int64_t acc[4];
+      oz2o_dot4_i8(A8 + (size_t)i * kp, b, b + kp, b + 2 * (size_t)kp, b + 3 * (size_t)kp, kp, acc);
+      for (int c = 0; c < 4; ++c) {
+        if (acc[c] > INT32_MAX || acc[c] < INT32_MIN) bad = 1;
+        C32[i + (size_t)(j + c) * m] = (int32_t)acc[c];
+      }
+    }
+  }
+  for (; j < n; ++j)
+    for (int i = 0; i < m; ++i) {
+      const int64_t acc = oz2o_dot_i8(A8 + (size_t)i * kp, B8 + (size_t)j * kp, kp);
       if (acc > INT32_MAX || acc < INT32_MIN) bad = 1;
       C32[i + (size_t)j * m] = (int32_t)acc;
     }

@@ -74,6 +74,10 @@ void oz2o_prep_cols(int n, int k, int N, const double* B, int ldb, int8_t* B8, i
 /* C32 (m x n column-major, ld m) = A8 (m x kp row-major) * B8 (n x kp row-major)^T, exact.
  * Returns 0, or 1 if an entry does not fit int32. */
 int oz2o_i8_gemm(int m, int n, int kp, const int8_t* A8, const int8_t* B8, int32_t* C32);
+/* Exact int8 dot products (oz2_i8dot.c): one of length n, and one row against four rows. */
+int64_t oz2o_dot_i8(const int8_t* a, const int8_t* b, int n);
+void oz2o_dot4_i8(const int8_t* a, const int8_t* b0, const int8_t* b1, const int8_t* b2, const int8_t* b3, int n,
+                  int64_t* out);
 
 /* Reconstruct one problem from its N+1 int32 planes (plane stride m*n).  cnt[0..3] +=
  * {unused, uncertified, repaired, safety_fallback}. */

@@ -202,6 +202,55 @@ def oracle_block(A_t, B_t, C0_t, k, alpha, beta, N, mode, I, J):
     return c, cnt
 
 
+def oracle_full_many(jobs, workers=16, batch=16):
+    """Every entry of several problems through the oracle, on a thread pool (the oracle is a ctypes
+    call, which releases the GIL; 16 workers = the host share of one GPU).  jobs: list of
+    (key, A_t, B_t, C0_t, k, alpha, beta, N, mode, I, J, got) with torch layouts as in oracle_block,
+    I / J row / column index arrays or None (all), got the device result's entries (|J|, |I|) as a
+    host array.  Yields (key, equal, counters, first differing (j, i) or None) per job; jobs are
+    taken in batches so that at most `batch` problems' host copies are alive at once."""
+    from concurrent.futures import ThreadPoolExecutor
+    t = torch()
+
+    def host_inputs(A_t, B_t, C0_t, k, beta, I, J):
+        if I is None:
+            a = np.ascontiguousarray(A_t[:k].cpu().numpy())
+            b = np.ascontiguousarray(B_t[:, :k].cpu().numpy())
+            c = (np.zeros(B_t.shape[0] * A_t.shape[1]).reshape(B_t.shape[0], A_t.shape[1])
+                 if C0_t is None or beta == 0.0 else np.ascontiguousarray(C0_t.cpu().numpy()))
+            return a, b, c
+        ii = t.as_tensor(np.asarray(I), device=A_t.device)
+        jj = t.as_tensor(np.asarray(J), device=A_t.device)
+        a = np.ascontiguousarray(A_t[:k][:, ii].cpu().numpy())
+        b = np.ascontiguousarray(B_t[jj][:, :k].cpu().numpy())
+        c = (np.zeros((len(J), len(I))) if C0_t is None or beta == 0.0 else
+             np.ascontiguousarray(C0_t[jj][:, ii].cpu().numpy()))
+        return a, b, c
+
+    def work(item):
+        key, (a, b, c), k, alpha, beta, N, mode, got = item
+        m, n = a.shape[1], b.shape[0]
+        cnt = np.zeros(4, dtype=np.int64)
+        rc = O.oracle().oz2o_emulate(m, n, k, N, a.reshape(-1), m, b.reshape(-1), k, c.reshape(-1), m, alpha, beta,
+                                     mode, cnt)
+        assert rc == 0, (key, rc)
+        eq = same_bits(got, c)
+        where = None
+        if not eq:
+            bad = ~((got.view(np.int64) == c.view(np.int64)) | (np.isnan(got) & np.isnan(c)))
+            where = tuple(int(x) for x in np.argwhere(bad)[0])
+        return key, eq, cnt, where
+
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        for b0 in range(0, len(jobs), batch):
+            items = []
+            for (key, A_t, B_t, C0_t, k, alpha, beta, N, mode, I, J, got) in jobs[b0:b0 + batch]:
+                items.append((key, host_inputs(A_t, B_t, C0_t, k, beta, I, J), k, alpha, beta, N, mode, got))
+            for r in pool.map(work, items):
+                yield r
+            del items
+
+
 def gpu_block(C_t, I, J):
     """Entries (I x J) of a device result in torch layout (n, >= m), as a (|J|, |I|) array."""
     t = torch()

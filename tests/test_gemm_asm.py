@@ -34,16 +34,6 @@ def test_checker_finds_a_pending_global_load():
     assert [t for _, t, _ in L.check_lines(asm(3), "k")] == ["v_cmp_ne_u32_e32 vcc, 0, v7"]
 
 
-def test_checker_finds_a_pending_global_load():
-    """A global load ahead of two LDS DMAs: vmcnt(2) covers it, vmcnt(3) does not."""
-    def asm(n):
-        return ["k:", "\tglobal_load_dword v7, v[2:3], off", "\tglobal_load_lds_dwordx4 v[4:5], off",
-                "\tglobal_load_lds_dwordx4 v[4:5], off", f"\ts_waitcnt vmcnt({n})", "\tv_cmp_ne_u32_e32 vcc, 0, v7",
-                "\ts_endpgm"]
-    assert L.check_lines(asm(2), "k") == []
-    assert [t for _, t, _ in L.check_lines(asm(3), "k")] == ["v_cmp_ne_u32_e32 vcc, 0, v7"]
-
-
 def test_int8_gemm_kernels_wait_before_use(tmp_path):
     out = tmp_path / "i8gemm.s"
     cmd = ["/opt/rocm/bin/hipcc", "-O3", "-std=c++17", "-fPIC", f"-I{REPO / 'include'}", f"-I{CSRC}", "-x", "hip",

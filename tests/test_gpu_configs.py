@@ -1,17 +1,21 @@
-"""The reference's benchmark configurations at full size, every emulated problem checked bit for bit
-against the oracle on sampled entries.
+"""The reference's benchmark configurations at full size, emulated problems checked bit for bit
+against the oracle: every entry of every emulated problem (uniform and ragged configs), every entry
+of the finite-row x finite-column block of every problem plus sampled entries elsewhere (hard
+config), sampled entries (large config, whose 1.5e14 multiply-adds the CPU oracle cannot redo).
 
 Each output entry of the Ozaki-II pipeline depends only on its row of A, its column of B and its C0
 entry (shifts, abs shifts and norm bounds are per row / column; CRT, certificate and repair per
 entry), so the oracle run on the sub-problem (rows I of A, columns J of B, C0(I, J)) gives the exact
-bits of those entries (tests/gpu_util.oracle_block).  Per emulated problem 8 rows x 8 columns are
-compared bit for bit, in COUNT mode (uncertified entries keep their emulated value, so an error in
-any stage shows) and in ON mode (repaired entries take the FP64 dot, whose bits the oracle also
-gives).  Native-route problems (own FP64 MFMA GEMM, whose order differs from the reference's closed
-vendor GEMM) are checked by the componentwise gamma_n gate against an 80-bit dot; alpha = 0 problems
-must equal beta C0 exactly.  Stats (fallback count, moduli range) must equal the oracle planner's,
-device counters must be consistent with the sampled oracle counts, and a repeated call must
-reproduce every bit.
+bits of those entries (tests/gpu_util.oracle_block).  Calls are checked in COUNT mode (uncertified
+entries keep their emulated value, so an error in any stage shows) and in ON mode (repaired entries
+take the FP64 dot, whose bits the oracle also gives).  Where the oracle covers every entry that can be
+uncertified or repaired, the device counters must EQUAL the oracle's counts (num_uncertified in COUNT
+mode, num_repaired in ON mode, num_safety_fallback), as the reference's numerics test requires
+(tests/test_numerics_standalone.cu:400-433); on the large config they must be at least the sampled
+counts.  Native-route problems (own FP64 MFMA GEMM, whose order differs from the reference's closed
+vendor GEMM) are checked by the componentwise gamma_n gate against an 80-bit dot on sampled entries;
+alpha = 0 problems must equal beta C0 exactly.  Stats (fallback count, moduli range) must equal the
+oracle planner's, and a repeated call must reproduce every bit.
 
   uniform : G = 64 x 1024^3, (U-0.5)exp(0.5Z), alpha 1, beta 0.5            (EMU_GROUPED and AUTO)
   ragged  : G = 128, m, n log-U[64, 4096], k log-U[16, 8192], 8 alpha = 0    (AUTO and EMU_GROUPED)
@@ -27,7 +31,7 @@ import torch
 
 import ggemm as G
 import oracle_lib as O
-from gpu_util import gpu_block, oracle_block, same_bits, say
+from gpu_util import gpu_block, oracle_block, oracle_full_many, read_counters, same_bits, say
 
 pytestmark = pytest.mark.gpu
 U53 = 2.0 ** -53
@@ -103,16 +107,43 @@ def pick(rng, size, count, prefer=None):
     return np.sort(rng.choice(size, count, replace=False))
 
 
-def check_problems(shapes, A, B, C0, Cw, plan, repair, rng, n_side=8, finite_masks=None):
-    """Sampled entries of every problem against the oracle (emulated routes, bitwise), the gamma_n
-    gate (native routes) or beta C0 (alpha = 0).  Returns the oracle counters summed over the
-    samples and the worst native err / gamma_n."""
+def check_full(shapes, A, B, C0, Cw, plan, repair, blocks=None):
+    """Every entry of every emulated problem bitwise against the oracle -- or, with blocks, the entries
+    of rows I x columns J of problem g, blocks[g] = (I, J) -- on a thread pool.  Returns the oracle's
+    counters [nonfinite vectors, uncertified, repaired, safety] summed over the entries covered."""
+    jobs = []
+    for g, (m, n, k, a, b) in enumerate(shapes):
+        e = plan[g]
+        if a == 0.0 or e.route != 0:
+            continue
+        I, J = blocks[g] if blocks is not None else (None, None)
+        if I is None:
+            assert tuple(A[g].shape) == (k, m) and tuple(B[g].shape) == (n, k) and tuple(Cw[g].shape) == (n, m)
+            got = Cw[g].cpu().numpy()
+        elif len(I) == 0 or len(J) == 0:
+            continue
+        else:
+            got = gpu_block(Cw[g], I, J)
+        jobs.append((g, A[g], B[g], C0[g], k, a, b, e.num_moduli, oz2_mode(repair), I, J, got))
+    tot = np.zeros(4, dtype=np.int64)
+    for g, eq, cnt, where in oracle_full_many(jobs):
+        assert eq, f"problem {g} {shapes[g][:3]} N={plan[g].num_moduli}: entry (column, row) {where} differs"
+        tot += cnt
+    return tot
+
+
+def check_problems(shapes, A, B, C0, Cw, plan, repair, rng, n_side=8, finite_masks=None, emulated=True):
+    """Sampled entries of every problem against the oracle (emulated routes, bitwise; skipped with
+    emulated=False), the gamma_n gate (native routes) or beta C0 (alpha = 0).  Returns the oracle
+    counters summed over the samples and the worst native err / gamma_n."""
     tot = np.zeros(4, dtype=np.int64)
     worst = 0.0
     for g, (m, n, k, a, b) in enumerate(shapes):
         e = plan[g]
         if a == 0.0:   # BLAS: beta C0 exactly, A and B not referenced
             assert torch.equal(Cw[g], b * C0[g]), g
+            continue
+        if e.route == 0 and not emulated:
             continue
         pr, pc = (finite_masks[g] if finite_masks else (None, None))
         I = pick(rng, m, n_side, pr)
@@ -138,13 +169,20 @@ def check_problems(shapes, A, B, C0, Cw, plan, repair, rng, n_side=8, finite_mas
     return tot, worst
 
 
-def check_stats(st, shapes, plan, sampled):
+def check_stats(st, shapes, plan, counts, exact):
+    """Routes and moduli as the oracle planner's; device counters equal to the oracle's counts
+    (exact: the oracle covered every entry that can be uncertified, repaired or safety) or at least
+    the sampled ones."""
     emu = [e.num_moduli for e in plan if e.route == 0]
     assert st.num_fallback == sum(O.oracle().oz2o_route_is_fallback(e.route) for e in plan)
     if emu:
         assert (st.moduli_min, st.moduli_max) == (min(emu), max(emu))
-    # the device counters cover every entry, the oracle's only the sampled ones
-    assert st.num_uncertified >= sampled[1] and st.num_repaired >= sampled[2] and st.num_safety_fallback >= sampled[3]
+    got = (st.num_uncertified, st.num_repaired, st.num_safety_fallback)
+    want = (int(counts[1]), int(counts[2]), int(counts[3]))
+    if exact:
+        assert got == want, f"device counters (uncertified, repaired, safety) {got} != oracle {want}"
+    else:
+        assert all(x >= y for x, y in zip(got, want)), (got, want)
 
 
 def run_call(h, path, cfg, probs, n):
@@ -184,10 +222,12 @@ def test_uniform_config_sampled_bitwise(path):
                 Cw[g].copy_(C0[g])
             st = run_call(h, path, cfg, probs, len(shapes))
             plan = oracle_plan(shapes, cfg, path)
-            sampled, worst = check_problems(shapes, A, B, C0, Cw, plan, repair, rng)
-            check_stats(st, shapes, plan, sampled)
+            counts = check_full(shapes, A, B, C0, Cw, plan, repair)
+            _, worst = check_problems(shapes, A, B, C0, Cw, plan, repair, rng, emulated=False)
+            check_stats(st, shapes, plan, counts, exact=True)
             say(f"  routes {sorted({G.ROUTES[e.route] for e in plan})}, moduli {st.moduli_min}..{st.moduli_max}, "
-                f"uncertified {st.num_uncertified}, repaired {st.num_repaired}, native worst err/gamma {worst:.3g}")
+                f"uncertified {st.num_uncertified}, repaired {st.num_repaired} (oracle, every entry: "
+                f"{counts.tolist()}), native worst err/gamma {worst:.3g}")
 
 
 @pytest.mark.parametrize("path", [G.PATH_AUTO, G.PATH_EMU_GROUPED])
@@ -217,11 +257,12 @@ def test_ragged_config_sampled_bitwise(path):
                 assert torch.equal(first[g].view(torch.int64), Cw[g].view(torch.int64)), f"call 2 differs ({g})"
             del first
             plan = oracle_plan(shapes, cfg, path)
-            sampled, worst = check_problems(shapes, A, B, C0, Cw, plan, repair, rng)
-            check_stats(st, shapes, plan, sampled)
+            counts = check_full(shapes, A, B, C0, Cw, plan, repair)
+            _, worst = check_problems(shapes, A, B, C0, Cw, plan, repair, rng, emulated=False)
+            check_stats(st, shapes, plan, counts, exact=True)
             say(f"  repair={repair}: routes {sorted({G.ROUTES[e.route] for e in plan})}, moduli "
                 f"{st.moduli_min}..{st.moduli_max}, fallback {st.num_fallback}, uncertified {st.num_uncertified}, "
-                f"repaired {st.num_repaired}, sampled oracle counts {sampled.tolist()}, native worst {worst:.3g}")
+                f"repaired {st.num_repaired}, oracle counts over every entry {counts.tolist()}, native worst {worst:.3g}")
 
 
 def test_large_config_plan_execute_pointer_updates_sampled_bitwise():
@@ -260,10 +301,16 @@ def test_large_config_plan_execute_pointer_updates_sampled_bitwise():
                     for (data, out, tag) in ((X, C1, "X -> C1"), (Y, C2, "Y -> C2"), (X, C2, "X -> C2")):
                         if tag != "X -> C1":
                             assert G.lib().ggemm_plan_update_pointers(plan, ptrs(data[0]), ptrs(data[1]), ptrs(out)) == 0
+                        read_counters(reset=True)
                         assert G.lib().ggemm_execute_plan(plan, None) == 0
                         torch.cuda.synchronize()
+                        dev = read_counters(reset=True)   # the device counters of this execution
                         sampled, _ = check_problems(shapes, data[0], data[1], [None] * Gp, out, oplan, repair, rng)
-                        say(f"  repair={repair} {tag}: sampled oracle counts {sampled.tolist()}")
+                        st.num_uncertified, st.num_repaired = dev.uncertified, dev.repaired
+                        st.num_safety_fallback = dev.safety_fallback
+                        check_stats(st, shapes, oplan, sampled, exact=False)
+                        say(f"  repair={repair} {tag}: sampled oracle counts {sampled.tolist()}, device uncertified "
+                            f"{dev.uncertified}, repaired {dev.repaired}, safety {dev.safety_fallback}")
                 finally:
                     G.lib().ggemm_destroy_plan(plan)
     finally:
@@ -274,11 +321,13 @@ def test_large_config_plan_execute_pointer_updates_sampled_bitwise():
 def test_hard_numerics_config_sampled_bitwise():
     """G = 32 x 2048^3 + 4 x 2048^2 x 65536, (U-0.5)exp(4Z), 0.1 % of A and B entries NaN / +-Inf,
     AUTO with repair ON (then COUNT).  Almost every row and column holds a non-finite value, so
-    nearly all entries take the FP64 safety path.  Checked: sampled entries bitwise against the
-    oracle (half the sampled rows / columns finite, so certified, repaired and safety entries are
-    all covered); on every entry C is non-finite exactly where row i of A or column j of B is; the
-    safety count equals the number of such entries of the emulated problems; routes as the oracle
-    planner's; a repeated call reproduces every bit."""
+    nearly all entries take the FP64 safety path.  Checked: every entry of each problem's
+    finite-row x finite-column block bitwise against the oracle -- the only entries that can be
+    certified, uncertified or repaired -- so num_repaired (ON) and num_uncertified (COUNT) must
+    equal the oracle's counts; sampled entries elsewhere bitwise too (safety entries); on every entry
+    C is non-finite exactly where row i of A or column j of B is; the safety count equals the number
+    of such entries of the emulated problems; routes as the oracle planner's; a repeated call
+    reproduces every bit."""
     shapes = [(2048, 2048, 2048, 1.0, 0.0)] * 32 + [(2048, 2048, 65536, 1.0, 0.0)] * 4
     g_ = torch.Generator(device="cuda")
     g_.manual_seed(5)
@@ -311,10 +360,14 @@ def test_hard_numerics_config_sampled_bitwise():
                     safety += m * n - int(rows_ok[g].sum()) * int(cols_ok[g].sum())
             sampled, worst = check_problems(shapes, A, B, [None] * len(shapes), Cw, plan, repair, rng,
                                             finite_masks=list(zip(rows_ok, cols_ok)))
-            check_stats(st, shapes, plan, sampled)
-            assert st.num_safety_fallback == safety
+            blocks = [(np.flatnonzero(r), np.flatnonzero(c)) for r, c in zip(rows_ok, cols_ok)]
+            counts = check_full(shapes, A, B, [None] * len(shapes), Cw, plan, repair, blocks=blocks)
+            assert counts[3] == 0
+            counts[3] = safety
+            check_stats(st, shapes, plan, counts, exact=True)
             if repair == G.REPAIR_ON:
                 assert st.num_uncertified == 0
             say(f"  repair={repair}: safety {safety}, repaired {st.num_repaired}, uncertified {st.num_uncertified}, "
                 f"fallback {st.num_fallback}, routes {sorted({G.ROUTES[e.route] for e in plan})}, moduli "
-                f"{st.moduli_min}..{st.moduli_max}, sampled oracle counts {sampled.tolist()}")
+                f"{st.moduli_min}..{st.moduli_max}, oracle counts over the finite blocks {counts.tolist()}, "
+                f"sampled {sampled.tolist()}")

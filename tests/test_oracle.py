@@ -29,6 +29,32 @@ MODULI = [256, 255, 253, 251, 247, 239, 233, 229, 227, 223, 217, 211, 199, 197, 
 
 
 # ------------------------------------------------------------------------------ CRT tables
+REFERENCE = Path("/root/reference")
+REF_LIB = Path(__file__).resolve().parents[1] / "oracle" / "_ref" / "libref_moduli.so"
+
+
+@pytest.mark.skipif(not (REFERENCE / "src" / "moduli.h").exists() and not REF_LIB.exists(),
+                    reason="the reference checkout (and so its table builder) is not on this host")
+def test_crt_tables_byte_identical_to_reference_build():
+    """The reference's own table builder (src/moduli.h:124-181, compiled unmodified by
+    `make -C oracle ref` into oracle/_ref/) and the oracle's restatement produce the same table,
+    byte for byte: moduli, Barrett magics, 2^e mod p, s1 / s2 splits, CRT inverses, P1, P2, u1 / P,
+    log2 u1, T_N and log2 P for every N (the ulp-level P2, inv_Pu and T_N included)."""
+    import subprocess
+    if (REFERENCE / "src" / "moduli.h").exists():
+        subprocess.run(["make", "-s", "-C", str(REF_LIB.parents[1]), "ref"], check=True)
+    ref = C.CDLL(str(REF_LIB))
+    ref.ref_crt_tables_size.restype = C.c_size_t
+    ref.ref_build_crt_tables.argtypes = [C.c_void_p, C.c_size_t]
+    size = ref.ref_crt_tables_size()
+    t = tables()
+    assert size == C.sizeof(t) == 10368
+    buf = C.create_string_buffer(size)
+    assert ref.ref_build_crt_tables(buf, size) == 0
+    ours = C.string_at(C.addressof(t), size)
+    assert buf.raw == ours, [i for i in range(size) if buf.raw[i] != ours[i]][:16]
+
+
 def test_crt_tables_exact_identities():
     t = tables()
     for a in range(20):
@@ -385,3 +411,33 @@ def test_planner_auto_num_moduli_and_costs():
             assert e.t_emu_s <= e.t_native_s
         if e.route == 5:
             assert e.t_emu_s > e.t_native_s
+
+
+# ------------------------------------------------------------------------- CPU baseline GEMM
+@pytest.mark.parametrize("m,n,k,lda_pad,alpha,beta", [(1, 1, 1, 0, 1.0, 0.0), (70, 33, 300, 5, -1.5, 0.5),
+                                                       (129, 65, 257, 0, 2.0, 1.0), (64, 32, 256, 3, 0.0, -0.75),
+                                                       (200, 97, 5, 0, 1.0, 0.0)])
+def test_cpu_baseline_dgemm_matches_numpy(m, n, k, lda_pad, alpha, beta):
+    """oracle/oz2_dgemm.c (the bench's timed CPU baseline): C = alpha A B + beta C, column-major with
+    leading dimensions above the row counts, block edges (m, n, k not multiples of the 64 / 32 / 256
+    blocks), alpha = 0, and beta = 0 never reading C (NaN there must not propagate).  Against numpy's
+    float64 product within the componentwise FP64 bound gamma_{k+2} (|alpha| |A| |B| + |beta C|)."""
+    rng = np.random.default_rng(m * 1000 + n * 10 + k)
+    lda, ldb, ldc = m + lda_pad, k + lda_pad, m + lda_pad
+    A = rng.standard_normal((k, lda))          # column-major m x k with leading dimension lda
+    B = rng.standard_normal((n, ldb))          # column-major k x n
+    C0 = rng.standard_normal((n, ldc))         # column-major m x n
+    if beta == 0.0:
+        C0[:, :m] = np.nan
+    Cw = C0.copy()
+    oracle().oz2o_dgemm(m, n, k, alpha, A.reshape(-1), lda, B.reshape(-1), ldb, beta, Cw.reshape(-1), ldc)
+    a, b = A[:, :m].T, B[:, :k].T               # m x k, k x n
+    c0 = np.zeros((m, n)) if beta == 0.0 else C0[:, :m].T
+    ref = alpha * (a @ b) + beta * c0
+    bound = abs(alpha) * (np.abs(a) @ np.abs(b)) + abs(beta) * np.abs(c0)
+    u = 2.0 ** -53
+    gam = (k + 2) * u / (1 - (k + 2) * u)
+    got = Cw[:, :m].T
+    assert np.all(np.isfinite(got))
+    assert np.all(np.abs(got - ref) <= 2 * gam * bound + 1e-300)
+    assert np.array_equal(Cw[:, m:], C0[:, m:], equal_nan=True)   # padding rows untouched

@@ -226,7 +226,8 @@ def test_plan_allocates_nothing(tmp_path):
     lib_dir = REPO / "coding-basic-hw-2_amd" / "ggemm"
     subprocess.run(["g++", "-O1", "-std=c++17", "-D__HIP_PLATFORM_AMD__", f"-I{REPO / 'include'}",
                     "-I/opt/rocm/include", str(REPO / "tests" / "planner_alloc" / "count_allocs.cpp"), "-o", str(exe),
-                    f"-L{lib_dir}", "-lggemm_mi355x", f"-Wl,-rpath,{lib_dir}"], check=True)
+                    f"-L{lib_dir}", "-lggemm_mi355x", f"-Wl,-rpath,{lib_dir}", "-L/opt/rocm/lib", "-lamdhip64"],
+                   check=True)
     r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stderr
     lines = [l for l in r.stdout.splitlines() if l.startswith("path=")]

@@ -113,3 +113,38 @@ def test_noalloc_rejects_beyond_limits():
         assert rc == G.GGEMM_ERR_INVALID, path
     rc, st, _ = noalloc(G.PATH_EMU_GROUPED, cfg, ok)   # still usable after the rejections
     assert rc == 0 and st.kernel_launches == 4
+
+
+def test_noalloc_refuses_a_capturing_stream():
+    """The entry point synchronises its stream, so it cannot be captured: on a stream under capture it
+    returns GGEMM_ERR_INVALID without touching the capture, which then ends normally (an empty graph);
+    the same stream then runs the call and matches a handle call bit for bit."""
+    hip = C.CDLL("libamdhip64.so")
+    case = Case([(64, 48, 100), (37, 29, 257)], 20261243, phi=1.0, beta=0.5)
+    cfg = G.Config(0, 1e-15, 1, G.REPAIR_ON)
+    stream = C.c_void_p()
+    assert hip.hipStreamCreate(C.byref(stream)) == 0
+    try:
+        say("noalloc under stream capture (global mode)")
+        case.reset_C()
+        arr = G.problems_array(case.problems())
+        torch.cuda.synchronize()
+        assert hip.hipStreamBeginCapture(stream, 0) == 0
+        st = G.Stats()
+        rc = G.lib().ggemm_grouped_dgemm_noalloc(G.PATH_AUTO, C.byref(cfg), arr, len(case.hp), stream, C.byref(st))
+        graph = C.c_void_p()
+        end = hip.hipStreamEndCapture(stream, C.byref(graph))
+        assert rc == G.GGEMM_ERR_INVALID, rc
+        assert end == 0 and graph.value, end
+        assert hip.hipGraphDestroy(graph) == 0
+        rc = G.lib().ggemm_grouped_dgemm_noalloc(G.PATH_AUTO, C.byref(cfg), arr, len(case.hp), stream, C.byref(st))
+        assert rc == 0, rc
+        assert hip.hipStreamSynchronize(stream) == 0
+        out = [case.C(g).copy() for g in range(len(case.hp))]
+        rc, sh, ref = with_handle(G.PATH_AUTO, cfg, case)
+        assert rc == 0
+        for g, (a, b) in enumerate(zip(out, ref)):
+            assert same_bits(a, b), f"problem {g} differs from the handle call"
+        assert same_stats(st, sh), (st.as_dict(), sh.as_dict())
+    finally:
+        hip.hipStreamDestroy(stream)
