@@ -253,16 +253,20 @@ def run_kernel(case, kernel, cfg=CFG_EMU, **env):
         return [case.C(g).copy() for g in range(len(case.hp))]
 
 
-@pytest.mark.parametrize("sched", ["dispatch", "persistent"])
+SCHED_ENV = {"dispatch": {}, "persistent": {"GGEMM_I8_SCHED": "persistent"}, "rowmajor": {"GGEMM_PACKED_MAX_KP": "0"}}
+
+
+@pytest.mark.parametrize("sched", ["dispatch", "persistent", "rowmajor"])
 @pytest.mark.parametrize("kernel", ["large", "general"])
 def test_large_tile_kernel_ragged_edges(kernel, sched):
     """The large-tile INT8 kernel (forced with GGEMM_I8_KERNEL; by default it serves long-k
-    calls) and the general kernel on the same products, each with one workgroup per tile and as
-    persistent work-stealing kernels (GGEMM_I8_SCHED=persistent): m, n are not multiples of 256
-    (clamped edge rows) and kp = 480 is 32 mod 64 (the zeroed half stage)."""
+    calls) and the general kernel on the same products, each with one workgroup per tile, as
+    persistent work-stealing kernels (GGEMM_I8_SCHED=persistent), and on row-major residues
+    (GGEMM_PACKED_MAX_KP=0: the large kernel's 128-byte stages): m, n are not multiples of 256
+    (clamped edge rows) and kp = 480 is 32 mod 64 and 96 mod 128 (the zeroed partial stages)."""
     case = Case([(520, 600, 470)] * 3, 20261206, phi=0.5, beta=0.5)
     say(f"{kernel} kernel, ragged edges, {sched}")
-    run_kernel(case, kernel, **({"GGEMM_I8_SCHED": "persistent"} if sched == "persistent" else {}))
+    run_kernel(case, kernel, **SCHED_ENV[sched])
 
 
 @pytest.mark.parametrize("kernel", ["large", "general"])
@@ -288,11 +292,12 @@ def test_persistent_kernels_ragged_group(kernel):
 
 @pytest.mark.parametrize("colmajor", [False, True])
 def test_large_tile_kernel_mixed_k_stream(colmajor):
-    """The large-tile kernel on products with 1 to 9 k-stages (kp = 64 .. 576, some 32 mod 64),
-    full tiles and a ragged n (edge stores), with the packed residues and blocked digits and with
-    the row-major / column-major layouts (GGEMM_DIGITS_COLMAJOR=1)."""
-    shapes = [(512, 512, 40), (512, 512, 64), (512, 512, 100), (512, 512, 160),
-              (512, 520, 300), (512, 512, 520), (512, 512, 576)]
+    """The large-tile kernel on products with 1 to 9 k-stages (kp = 64 .. 576; kp mod 128 = 0, 32,
+    64 and 96, the final partial stages of the 128-byte stages that row-major residues take), full
+    tiles and a ragged n (edge stores), with the packed residues and blocked digits (64-byte
+    stages) and with the row-major / column-major layouts (GGEMM_DIGITS_COLMAJOR=1)."""
+    shapes = [(512, 512, 40), (512, 512, 64), (512, 512, 100), (512, 512, 160), (512, 512, 224),
+              (512, 520, 300), (512, 512, 350), (512, 512, 520), (512, 512, 576)]
     case = Case(shapes, 20261207, phi=0.5, beta=0.5)
     say(f"large-tile kernel, mixed k stream, colmajor={colmajor}")
     run_kernel(case, "large", **({"GGEMM_DIGITS_COLMAJOR": "1"} if colmajor else {}))
@@ -403,11 +408,12 @@ def test_hard_numerics_nan_inf_and_repair():
     check_case(case, G.PATH_AUTO, CFG_AUTO, st, O.REPAIR_ON)
 
 
-@pytest.mark.parametrize("sched", ["dispatch", "persistent"])
+@pytest.mark.parametrize("sched", ["dispatch", "persistent", "rowmajor"])
 @pytest.mark.parametrize("kernel", ["large", "general"])
 def test_nonfinite_tiles_skipped(kernel, sched):
     """INT8 GEMM tiles whose rows (or columns) are all non-finite are not computed by the
-    dispatched kernels (every entry takes the safety fallback); the persistent kernels compute
+    dispatched kernels (every entry takes the safety fallback; on packed and, with
+    GGEMM_PACKED_MAX_KP=0, on row-major residues); the persistent kernels compute
     them.  Either way the bits and counters are the oracle's: a problem with a non-finite value
     in every A row, one whose first 256 B columns are non-finite (later columns finite), one whose
     first 256 A rows are non-finite, a short-k problem with every row non-finite (below the
@@ -429,8 +435,7 @@ def test_nonfinite_tiles_skipped(kernel, sched):
     spoil_rows(case.hp[3], range(100))
     case.alloc()
     say(f"non-finite tiles, {kernel} kernel, {sched}")
-    env = {"GGEMM_I8_SCHED": "persistent"} if sched == "persistent" else {}
-    run_kernel(case, kernel, **env)
+    run_kernel(case, kernel, **SCHED_ENV[sched])
     say("non-finite tiles, default kernel, repair ON")
     cfg = G.Config(0, 1e-15, 1, G.REPAIR_ON)
     rc, st = run(case, G.PATH_EMU_GROUPED, cfg)
