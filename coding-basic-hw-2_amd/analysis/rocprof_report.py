@@ -45,15 +45,16 @@ STAGES = ("prep", "i8_gemm", "reconstruct", "native", "memops")
 _STAGE_RE = [
     (re.compile(r"\bprep_kernel\b"), "prep"),
     (re.compile(r"\bi8_(grouped|large)(_persistent)?_kernel\b"), "i8_gemm"),
-    (re.compile(r"\b(recon|dots)_kernel\b"), "reconstruct"),
+    (re.compile(r"\b(recon|dots|gather|cross)_kernel\b"), "reconstruct"),
     (re.compile(r"\bf64_\w*kernel\b"), "native"),
     (re.compile(r"copyBuffer|fillBuffer|__amd_rocclr"), "memops"),
 ]
 
 
 # The kernel of each stage that the stage's algorithmic amount is credited to.  The reconstruct
-# stage's second kernel (dots_kernel, the FP64 dot products of flagged entries) does work that
-# depends on the data (how many entries the certificate rejects), so it gets no roofline column.
+# stage's other kernels (dots_kernel, gather_kernel and cross_kernel: the FP64 dot products of flagged entries) do
+# work that depends on the data (how many entries the certificate rejects), so they get no roofline
+# column.
 ALG_KERNEL = {"prep": r"\bprep_kernel\b", "i8_gemm": r"\bi8_", "reconstruct": r"\brecon_kernel\b"}
 
 

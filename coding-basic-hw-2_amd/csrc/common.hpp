@@ -197,17 +197,29 @@ struct YDesc {
   const int32_t* L;
   uint64_t* F;
   int32_t* nf;
-  int t0, d0;
+  // crossings sets of the dot pass (blocked layout): ceil(m / 64) row words, ceil(n / 64) column
+  // words and one word of counts, behind the flags; AT: row-major copies of the crossings rows in
+  // the residue workspace (free once the INT8 GEMM is done), nullptr: the dot pass defers nothing
+  uint64_t* X;
+  double* AT;
+  int t0, d0, b0, x0;   // the problem's first workgroup in the reconstruct, dot-pass, row-band and
+                        // crossings grids
+  int xn;               // the problem's crossings workgroups
   int nff, fla;
 };
 // Compact grids of a grouped call (ne problems): tiles in all and, when every problem has the same
-// count, that count (else 0) -- for the reconstruct and for the dot-product pass.
+// count, that count (else 0) -- for the reconstruct, the dot-product pass, the row bands of its
+// crossings pass and the crossings pass's workgroups.
 struct ReconGrid {
-  int ne, tiles, per, dtiles, dper;
+  int ne, tiles, per, dtiles, dper, bands, bper, xwgs, xper;
 };
 // Reconstruct tile shapes (rows x columns per workgroup): blocked digits / column-major, and the
 // dot-product pass's tile
 constexpr int kReconTileMB = 64, kReconTileNB = 16, kReconTileMC = 128, kReconTileNC = 8, kDotTile = 64;
+// Bytes of a problem's flags plus its crossings sets (blocked layout)
+inline size_t flag_bytes(int m, int n, size_t plane_entries) {
+  return plane_entries / 8 + sizeof(uint64_t) * (size_t)((m + 63) / 64 + (n + 63) / 64 + 1);
+}
 // Prep workgroup shapes: rows of A per A-row block, columns of B per B-column block
 constexpr int kPrepRows = 32, kPrepCols = 8;
 
@@ -242,8 +254,9 @@ int prep_launch(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t
 // problem, as wide as the largest problem's tile count (kernel-level API, per-problem launches).
 // dot_form: the dot-product pass's choice of forms -- kDotFormAuto, or for tests kDotFormDense (every
 // tile with flagged entries computes all its chains), kDotFormBlocks (per-block and listed entries
-// only), kDotFormList (listed entries only)
-enum { kDotFormAuto = 0, kDotFormDense = 1, kDotFormBlocks = 2, kDotFormList = 3 };
+// only), kDotFormList (listed entries only), kDotFormTile (as auto, but no tile defers its chains
+// to the crossings pass)
+enum { kDotFormAuto = 0, kDotFormDense = 1, kDotFormBlocks = 2, kDotFormList = 3, kDotFormTile = 4 };
 int recon_launch(const oz2_problem* d, const YDesc* yd, int num, int max_m, int max_n, hipStream_t s, int mode,
                  bool blocked = false, int* launches = nullptr, const ReconGrid* grid = nullptr,
                  int dot_form = kDotFormAuto);

@@ -249,7 +249,7 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
     SY += align_up((size_t)p.m * p.n, kBufAlign);
     SYb += align_up(blocked_plane_entries(p.m, p.n), kBufAlign);
     SLb += align_up(blocked_plane_entries(p.m, p.n), kBufAlign / 4) * sizeof(int32_t);
-    SFb += align_up(blocked_plane_entries(p.m, p.n) / 8, kBufAlign);
+    SFb += align_up(flag_bytes(p.m, p.n, blocked_plane_entries(p.m, p.n)), kBufAlign);
     SNF += align_up((size_t)(p.m + p.n) * kNfWords * sizeof(int32_t), kBufAlign);
   }
   c.blocked = !h->digits_colmajor && (size_t)nmax * SYb + SLb + SFb <= h->C32_bytes;
@@ -275,7 +275,7 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
   int32_t* lbase = reinterpret_cast<int32_t*>(ybase + (size_t)nmax * SY);
   uint8_t* fbase = reinterpret_cast<uint8_t*>(lbase) + SLb;
   uint8_t* nbase = fbase + SFb;
-  size_t oa = 0, ob = 0, orow = 0, ocol = 0, q = 0, oy = 0, ol = 0, of = 0, onf = 0;
+  size_t oa = 0, ob = 0, orow = 0, ocol = 0, q = 0, oy = 0, ol = 0, of = 0, onf = 0, oat = 0;
   for (int j = 0; j < c.ne; ++j) {
     const int g = emu_idx[j];
     const ggemm_problem_t& p = probs[g];
@@ -304,20 +304,34 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
     yd.L = lbase + ol;
     yd.F = c.blocked ? reinterpret_cast<uint64_t*>(fbase + of) : nullptr;
     yd.nf = nfsum ? reinterpret_cast<int32_t*>(nbase + onf) : nullptr;
+    yd.X = c.blocked ? reinterpret_cast<uint64_t*>(fbase + of + blocked_plane_entries(p.m, p.n) / 8) : nullptr;
+    {   // the gather workspace: the problem's m k doubles in the residue planes, while they last
+      const size_t at = align_up((size_t)p.m * (size_t)p.k * sizeof(double), kBufAlign);
+      yd.AT = nullptr;
+      if (c.blocked && oat + at <= h->A8_bytes) {
+        yd.AT = reinterpret_cast<double*>(reinterpret_cast<char*>(h->A8) + oat);
+        oat += at;
+      }
+    }
     yd.nff = 0;
     yd.fla = 0;
     {   // compact reconstruct / dot-product grids
       const int rm = c.blocked ? kReconTileMB : kReconTileMC, rn = c.blocked ? kReconTileNB : kReconTileNC;
       const long long rt = (long long)((p.m + rm - 1) / rm) * ((p.n + rn - 1) / rn);
       const long long dt = c.blocked ? (long long)((p.m + kDotTile - 1) / kDotTile) * ((p.n + kDotTile - 1) / kDotTile) : 0;
+      const long long bt = c.blocked ? (long long)((p.m + kDotTile - 1) / kDotTile) : 0;   // row bands
       ReconGrid& rg = c.rgrid;
-      if (rg.tiles + rt > 0x7fffffffLL || rg.dtiles + dt > 0x7fffffffLL) return GGEMM_ERR_INVALID;
+      if (rg.tiles + rt > 0x7fffffffLL || rg.dtiles + dt > 0x7fffffffLL || rg.bands + bt > 0x7fffffffLL)
+        return GGEMM_ERR_INVALID;
       yd.t0 = rg.tiles;
       yd.d0 = rg.dtiles;
+      yd.b0 = rg.bands;
       rg.per = j == 0 ? (int)rt : (rg.per == (int)rt ? rg.per : 0);
       rg.dper = j == 0 ? (int)dt : (rg.dper == (int)dt ? rg.dper : 0);
+      rg.bper = j == 0 ? (int)bt : (rg.bper == (int)bt ? rg.bper : 0);
       rg.tiles += (int)rt;
       rg.dtiles += (int)dt;
+      rg.bands += (int)bt;
       rg.ne = j + 1;
     }
     o.C32 = lbase + ol; o.c32_mod_stride = 0;   // the reconstruct reads yd, not C32
@@ -343,7 +357,7 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
     const size_t plane = c.blocked ? blocked_plane_entries(p.m, p.n) : (size_t)p.m * p.n;
     oy += align_up(plane, kBufAlign);
     ol += align_up(plane, kBufAlign / 4);
-    of += align_up(blocked_plane_entries(p.m, p.n) / 8, kBufAlign);
+    of += align_up(flag_bytes(p.m, p.n, blocked_plane_entries(p.m, p.n)), kBufAlign);
     onf += align_up((size_t)(p.m + p.n) * kNfWords * sizeof(int32_t), kBufAlign);
     oa += align_up((size_t)p.m * kp, kBufAlign);
     ob += align_up((size_t)p.n * kp, kBufAlign);
@@ -351,6 +365,24 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
     ocol += align_up((size_t)OZ2_ROW_WS_PER_ROW * p.n, 64);
     c.max_m = std::max(c.max_m, p.m);
     c.max_n = std::max(c.max_n, p.n);
+  }
+  if (c.blocked && c.ne > 0) {
+    // crossings workgroups: about 4 per CU over the call, each problem's share in proportion to its
+    // dot-pass tiles (at least one, at most one per tile); a workgroup loops over its problem's tiles
+    ReconGrid& rg = c.rgrid;
+    const long long budget = 4LL * std::max(1, h->num_cus), T = std::max(1, rg.dtiles);
+    long long x0 = 0;
+    for (int j = 0; j < c.ne; ++j) {
+      YDesc& yd = hyd[j];
+      const long long dt = (j + 1 < c.ne ? hyd[j + 1].d0 : rg.dtiles) - yd.d0;
+      const long long xn = std::max(1LL, std::min(dt, (budget * dt + T - 1) / T));
+      if (x0 + xn > 0x7fffffffLL) return GGEMM_ERR_INVALID;
+      yd.x0 = (int)x0;
+      yd.xn = (int)xn;
+      rg.xper = j == 0 ? (int)xn : (rg.xper == (int)xn ? rg.xper : 0);
+      x0 += xn;
+    }
+    rg.xwgs = (int)x0;
   }
   if (rp) {
     // prep descriptors (src/ggemm.cu:544-569): unique A as A-only problems (n = 0), then unique B
@@ -815,6 +847,7 @@ extern "C" int ggemm_create_ex(ggemm_handle_t* out, int max_problems, size_t max
                 : !std::strcmp(edf, "dense")  ? kDotFormDense
                 : !std::strcmp(edf, "blocks") ? kDotFormBlocks
                 : !std::strcmp(edf, "list")   ? kDotFormList
+                : !std::strcmp(edf, "tile")   ? kDotFormTile
                                               : kDotFormAuto;
   if (hipStreamSynchronize(stream) != hipSuccess) FAIL(GGEMM_ERR_CUDA);
 #undef HIPA

@@ -256,7 +256,13 @@ __device__ __forceinline__ void tile_dots(const oz2_problem& pr, int r0, int cb,
 // tiles of all problems back to back; per > 0: every problem has per tiles, else the problem is the
 // last one whose first tile, yds[p].t0 or .d0, is at most blockIdx.x); ne == 0: problem blockIdx.y,
 // tile blockIdx.x.
-template <bool kDots>
+// kGrid: 0 reconstruct tiles (t0), 1 dot-pass tiles (d0), 2 64-row bands (b0), 3 crossings workgroups
+// (x0).
+template <int kGrid>
+__device__ __forceinline__ int grid_first(const YDesc& y) {
+  return kGrid == 0 ? y.t0 : (kGrid == 1 ? y.d0 : (kGrid == 2 ? y.b0 : y.x0));
+}
+template <int kGrid>
 __device__ __forceinline__ void grid_tile(const YDesc* __restrict__ yds, int ne, int per, int& p, int& lt) {
   const int g = blockIdx.x;
   if (ne == 0) {
@@ -269,10 +275,10 @@ __device__ __forceinline__ void grid_tile(const YDesc* __restrict__ yds, int ne,
     int lo = 0, hi = ne - 1;
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
-      if ((kDots ? yds[mid].d0 : yds[mid].t0) <= g) lo = mid; else hi = mid - 1;
+      if (grid_first<kGrid>(yds[mid]) <= g) lo = mid; else hi = mid - 1;
     }
     p = lo;
-    lt = g - (kDots ? yds[lo].d0 : yds[lo].t0);
+    lt = g - grid_first<kGrid>(yds[lo]);
   }
 }
 
@@ -283,7 +289,7 @@ __global__ void __launch_bounds__(kThreads) recon_kernel(const oz2_problem* __re
                                                          unsigned long long* __restrict__ cnt, int gne, int gper) {
   __shared__ unsigned long long red[3][kThreads / 64];
   int pi, lt;
-  grid_tile<false>(yds, gne, gper, pi, lt);
+  grid_tile<0>(yds, gne, gper, pi, lt);
   const oz2_problem& pr = probs[pi];
   const int N = pr.num_moduli;
   const int m = pr.m, n = pr.n, K = pr.k;
@@ -304,6 +310,11 @@ __global__ void __launch_bounds__(kThreads) recon_kernel(const oz2_problem* __re
     lc = threadIdx.x >> 5;
   }
   const int i0 = r0 + lr, j = cb + lc;
+  if (kBlocked && threadIdx.x == 0 && m > 0 && n > 0) {   // clear the crossings sets for dots_kernel
+    GLOBAL uint64_t* const X = gpw(yds[pi].X);
+    if (cb == 0 && r0 < m) X[r0 >> 6] = 0ull;
+    if (r0 == 0 && (cb & 63) == 0 && cb < n) X[((m + 63) >> 6) + (cb >> 6)] = 0ull;
+  }
   const bool active = N >= 1 && N <= kMaxModuli && m > 0 && n > 0 && i0 < m && j < n;
   const double alpha = pr.alpha, beta = pr.beta;
   const int ne = active ? min(4, m - i0) : 0;
@@ -525,6 +536,7 @@ constexpr int kDK = 8;             // dense k-chunk
 constexpr int kSG = 16;            // sparse: entries per group
 constexpr int kListCap = 256;      // sparse list capacity (16 blocks x 3 lanes x 4 entries fit)
 constexpr int kCompactMax = 256;   // compact form: rows x columns of the flagged entries, one chain per thread
+constexpr int kBandMin = 8;        // flagged entries from which a compact tile defers to the crossings pass
 constexpr int kWaveLds = 16 * kKC + 16 * (kKC + 1);   // doubles of one wave's wave_dots staging
 constexpr int kUnion = 4 * kWaveLds;                  // wave_dots x 4 waves; >= dense, sparse
 static_assert(4 * kDK * kRT <= kUnion && 2 * 1024 <= kUnion, "dot-pass LDS union");
@@ -835,7 +847,7 @@ __global__ void __launch_bounds__(kThreads, 6) dots_kernel(const oz2_problem* __
   __shared__ unsigned long long rcm[2];   // tile rows / columns holding flagged entries
   __shared__ uint8_t rmap[kRT], cmap[kRT];
   int pi, lt;
-  grid_tile<true>(yds, gne, gper, pi, lt);
+  grid_tile<1>(yds, gne, gper, pi, lt);
   const oz2_problem& pr = probs[pi];
   const int N = pr.num_moduli;
   const int m = pr.m, n = pr.n;
@@ -847,6 +859,62 @@ __global__ void __launch_bounds__(kThreads, 6) dots_kernel(const oz2_problem* __
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const double alpha = pr.alpha, beta = pr.beta;
   const int mb = (m + 15) >> 4;
+  // Problems with NaN / Inf rows or columns (nff; the only ones with safety-fallback entries):
+  // the summaries of the thread's row (il = t % 64) and of the tile's column t (threads 0 .. 63) are
+  // loaded with the flag words, whether or not the tile turns out to need them (in bounds for
+  // every row and column; a finite row's words are never used), so that the safety evaluation
+  // below starts without a chain of dependent loads.
+  const GLOBAL int32_t* const nf = gp(yds[pi].nf);
+  const bool nfp = nf != nullptr && yds[pi].nff != 0;   // workgroup-uniform
+  const int il = t & 63, i = r0 + il;
+  // word q of a summary held in four int4 values (passed by value: an array whose address a helper
+  // takes stays in scratch; q is known at compile time after unrolling)
+  static_assert(kNfWords == 16, "summaries of four int4");
+  auto word = [](v4i a, v4i b, v4i c, v4i d, int q) __attribute__((always_inline)) {
+    const v4i x = q < 4 ? a : (q < 8 ? b : (q < 12 ? c : d));
+    return (q & 3) == 0 ? x.x : ((q & 3) == 1 ? x.y : ((q & 3) == 2 ? x.z : x.w));
+  };
+  int* const cinf = reinterpret_cast<int*>(buf);   // [64][4]: non-finite column, h word, exponent, listed
+  int* const clst = cinf + 4 * kRT;                // [64][kNfCap]: the column's infinities
+  v4i rw0 = v4i{0, 0, 0, 0}, rw1 = rw0, rw2 = rw0, rw3 = rw0;
+  int rsh = 0, rsg = 0;
+  if (nfp) {
+    if (i < m) {
+      const GLOBAL int32_t* rs = gp(pr.row_shift);
+      rsh = rs[i];
+      rsg = rs[m + i];
+      const GLOBAL v4i* R = reinterpret_cast<const GLOBAL v4i*>(nf + (size_t)kNfWords * i);
+      rw0 = R[0];
+      rw1 = R[1];
+      rw2 = R[2];
+      rw3 = R[3];
+    }
+    if (t < kRT) {   // column c0 + t: its summary to LDS (read after the flag count's barrier)
+      int cnf = 0, hc = 0, eB = kNfNoFinite, nc = 0;
+      const int j = c0 + t;
+      if (j < n) {
+        const GLOBAL int32_t* cs = gp(pr.col_shift);
+        const int csh = cs[j], ctau = cs[n + j];
+        const GLOBAL v4i* Cl = reinterpret_cast<const GLOBAL v4i*>(nf + (size_t)kNfWords * ((size_t)m + j));
+        const v4i cw0 = Cl[0], cw1 = Cl[1], cw2 = Cl[2], cw3 = Cl[3];
+        if (csh == OZ2_SHIFT_NONFINITE) {
+          cnf = 1;
+          hc = cw0.x;
+          eB = cw0.y;
+          nc = min((hc >> 8) & 0xff, kNfCap);
+#pragma unroll
+          for (int s = 0; s < kNfCap; ++s)
+            if (s < nc) clst[t * kNfCap + s] = word(cw0, cw1, cw2, cw3, 2 + s);
+        } else {
+          eB = ctau == OZ2_SHIFT_ZERO ? kNfNoFinite : 6 - ctau;
+        }
+      }
+      cinf[4 * t] = cnf;
+      cinf[4 * t + 1] = hc;
+      cinf[4 * t + 2] = eB;
+      cinf[4 * t + 3] = nc;
+    }
+  }
   if (t < 64) {   // word t % 4 of block t / 4 = (bi, bj) = (t / 4 % 4, t / 16)
     const int bi = (r0 >> 4) + ((t >> 2) & 3), bj = (c0 >> 4) + (t >> 4);
     fl[t] = (bi < mb && bj * 16 < n) ? gp(yds[pi].F)[4 * ((size_t)bj * mb + bi) + (t & 3)] : 0ull;
@@ -859,56 +927,32 @@ __global__ void __launch_bounds__(kThreads, 6) dots_kernel(const oz2_problem* __
   lds_sync();
   int total = cnt[0];
   if (total == 0) return;   // workgroup-uniform
-  const GLOBAL int32_t* const nf = gp(yds[pi].nf);
-  if (nf) {
-    // safety-fallback entries from the summaries (nf_dot's rule): thread t takes row il = t % 64 of
-    // the tile in columns jl = 16 (t / 64) .. + 15; decided entries are stored and their flags
-    // cleared.  The tile's 64 column summaries are staged in LDS once, a thread keeps its row's
-    // summary and infinity list in registers, and the partner loads of its entries are issued
-    // together (8 at a time), one listed infinity after the other (entry after entry they were
-    // chains of dependent loads, flag -> column summary -> list -> partner).
-    const GLOBAL int32_t* rs = gp(pr.row_shift);
-    const GLOBAL int32_t* cs = gp(pr.col_shift);
-    int* const cinf = reinterpret_cast<int*>(buf);   // [64][4]: non-finite column, h word, exponent, listed
-    int* const clst = cinf + 4 * kRT;                // [64][kNfCap]: the column's infinities
-    if (t < kRT) {
-      const int j = c0 + t;
-      int cnf = 0, hc = 0, eB = kNfNoFinite, nc = 0;
-      if (j < n) {
-        if (cs[j] == OZ2_SHIFT_NONFINITE) {
-          const GLOBAL int32_t* Cl = nf + (size_t)kNfWords * ((size_t)m + j);
-          cnf = 1;
-          hc = Cl[0];
-          eB = Cl[1];
-          nc = min((hc >> 8) & 0xff, kNfCap);
-#pragma unroll
-          for (int s = 0; s < kNfCap; ++s)
-            if (s < nc) clst[t * kNfCap + s] = Cl[2 + s];
-        } else {
-          const int tau = cs[n + j];
-          eB = tau == OZ2_SHIFT_ZERO ? kNfNoFinite : 6 - tau;
-        }
-      }
-      cinf[4 * t] = cnf;
-      cinf[4 * t + 1] = hc;
-      cinf[4 * t + 2] = eB;
-      cinf[4 * t + 3] = nc;
+  // The tile had flags.  On every way out it leaves in the global flags exactly the entries it
+  // defers to the crossings pass (cross_kernel): the remaining flags when it defers, zeros otherwise.
+  GLOBAL uint64_t* const Fg = gpw(yds[pi].F);
+  auto publish = [&](bool deferred) {
+    if (t < 64) {
+      const int bi = (r0 >> 4) + ((t >> 2) & 3), bj = (c0 >> 4) + (t >> 4);
+      if (bi < mb && bj * 16 < n) Fg[4 * ((size_t)bj * mb + bi) + (t & 3)] = deferred ? fl[t] : 0ull;
     }
-    lds_sync();
-    const int il = t & 63, i = r0 + il, jb = 16 * (t >> 6);
+  };
+  if (nfp) {
+    // safety-fallback entries from the summaries (nf_dot's rule): thread t takes row il of the tile
+    // in columns jl = 16 (t / 64) .. + 15; decided entries are stored and their flags cleared.  The
+    // tile's 64 column summaries are in LDS, a thread keeps its row's in registers, and the
+    // partner loads for one listed infinity go out four entries at a time, row infinities and
+    // column infinities together.
+    const int jb = 16 * (t >> 6);
     const int K = pr.k;
     const int lk = K > 1 ? 32 - __clz(K - 1) : 0;
     unsigned cand = 0u, nanm = 0u, posm = 0u, negm = 0u;   // bit q: column jb + q
     int hr = 0, eA = kNfNoFinite, nr = 0;
-    int rl[kNfCap] = {};
     if (i < m) {
-      const int rsh = rs[i], sg = rs[m + i];
       const bool rnf = rsh == OZ2_SHIFT_NONFINITE;
-      const GLOBAL int32_t* R = nf + (size_t)kNfWords * i;
-      eA = sg == OZ2_SHIFT_ZERO ? kNfNoFinite : 6 - sg;
+      eA = rsg == OZ2_SHIFT_ZERO ? kNfNoFinite : 6 - rsg;
       if (rnf) {
-        hr = R[0];
-        eA = R[1];
+        hr = rw0.x;
+        eA = rw0.y;
       }
 #pragma unroll
       for (int q = 0; q < 16; ++q) {
@@ -926,8 +970,6 @@ __global__ void __launch_bounds__(kThreads, 6) dots_kernel(const oz2_problem* __
         cand |= 1u << q;
       }
       nr = cand ? min((hr >> 8) & 0xff, kNfCap) : 0;
-#pragma unroll
-      for (int s = 0; s < kNfCap; ++s) rl[s] = s < nr ? R[2 + s] : 0;
     }
     // a partner x of an infinity of sign ng: NaN for 0 or NaN, else the product's sign
     auto cls = [&](double x, bool ng, int q) {   // selects, not branches (no mask array in scratch)
@@ -937,48 +979,44 @@ __global__ void __launch_bounds__(kThreads, 6) dots_kernel(const oz2_problem* __
       negm |= (!z && o) ? b : 0u;
       posm |= (!z && !o) ? b : 0u;
     };
-    // row infinities: B(w, j) of every candidate entry, one listed infinity at a time
-    int nrm = nr;
+    // listed infinity s of the row (B(w, j) for every candidate column j) and of each column
+    // (A(i, w); a wave's 16 columns are the same in every lane)
+    int nrm = nr, ncm = 0;
 #pragma unroll
     for (int o = 32; o; o >>= 1) nrm = max(nrm, __shfl_xor(nrm, o));
+#pragma unroll
+    for (int q = 0; q < 16; ++q) ncm = max(ncm, cinf[4 * (jb + q) + 3]);
+    const int sm = max(nrm, ncm);   // wave-uniform
     const GLOBAL double* const Bg = gp(pr.B);
     const GLOBAL double* const Ag = gp(pr.A);
     const size_t ldb = (size_t)pr.ldb, lda = (size_t)pr.lda;
+    const int jbu = 16 * __builtin_amdgcn_readfirstlane(t >> 6);   // jb, known uniform
+#pragma unroll 1
+    for (int s = 0; s < sm; ++s) {   // wave-uniform trip count
+      {
+        const bool ract = s < nr;
+        int wr = 0;   // word 2 + s of the row summary (s is not a compile-time index here)
 #pragma unroll
-    for (int s = 0; s < kNfCap; ++s) {
-      if (s < nrm) {   // wave-uniform
-        const bool act = s < nr;
-        const int w = rl[s];
+        for (int q = 0; q < kNfCap; ++q) wr = q == s ? word(rw0, rw1, rw2, rw3, 2 + q) : wr;
+        wr = ract ? wr : 0;
 #pragma unroll
-        for (int h = 0; h < 16; h += 8) {   // 8 loads in flight at a time (the kernel's register budget)
-          double x[8];
+        for (int h = 0; h < 16; h += 4) {   // 4 + 4 loads at a time (the kernel's register budget)
+          double xr[4], xc[4];
+          int wc[4];
 #pragma unroll
-          for (int q = 0; q < 8; ++q)
-            x[q] = (act && ((cand >> (h + q)) & 1u)) ? Bg[(size_t)(w & 0x7fffffff) + (size_t)(c0 + jb + h + q) * ldb] : 0.0;
+          for (int q = 0; q < 4; ++q) {
+            const bool rq = ract && ((cand >> (h + q)) & 1u);
+            xr[q] = rq ? Bg[(size_t)(wr & 0x7fffffff) + (size_t)(c0 + jbu + h + q) * ldb] : 0.0;
+            const bool cq = ((cand >> (h + q)) & 1u) && s < cinf[4 * (jb + h + q) + 3];
+            wc[q] = cq ? clst[(jb + h + q) * kNfCap + s] : 0;
+            xc[q] = cq ? Ag[(size_t)i + (size_t)(wc[q] & 0x7fffffff) * lda] : 0.0;
+          }
 #pragma unroll
-          for (int q = 0; q < 8; ++q)
-            if (act && ((cand >> (h + q)) & 1u)) cls(x[q], w < 0, h + q);
+          for (int q = 0; q < 4; ++q) {
+            if (ract && ((cand >> (h + q)) & 1u)) cls(xr[q], wr < 0, h + q);
+            if (((cand >> (h + q)) & 1u) && s < cinf[4 * (jb + h + q) + 3]) cls(xc[q], wc[q] < 0, h + q);
+          }
         }
-      }
-    }
-    // column infinities: A(i, w); a wave's 16 columns are the same in every lane
-    int ncm = 0;
-#pragma unroll
-    for (int q = 0; q < 16; ++q) ncm = max(ncm, cinf[4 * (jb + q) + 3]);
-    for (int s = 0; s < ncm; ++s) {   // wave-uniform trip count
-#pragma unroll
-      for (int h = 0; h < 16; h += 8) {
-        double x[8];
-        int wv[8];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const bool act = ((cand >> (h + q)) & 1u) && s < cinf[4 * (jb + h + q) + 3];
-          wv[q] = act ? clst[(jb + h + q) * kNfCap + s] : 0;
-          x[q] = act ? Ag[(size_t)i + (size_t)(wv[q] & 0x7fffffff) * lda] : 0.0;
-        }
-#pragma unroll
-        for (int q = 0; q < 8; ++q)
-          if (((cand >> (h + q)) & 1u) && s < cinf[4 * (jb + h + q) + 3]) cls(x[q], wv[q] < 0, h + q);
       }
     }
     // decided entries: NaN if a NaN factor, a zero / NaN partner or products of both signs
@@ -997,22 +1035,33 @@ __global__ void __launch_bounds__(kThreads, 6) dots_kernel(const oz2_problem* __
           const bool isnan_ = ((nanm >> (h + q)) & 1u) || (((posm & negm) >> (h + q)) & 1u);
           const double d = isnan_ ? __builtin_nan("") : (((posm >> (h + q)) & 1u) ? __builtin_inf() : -__builtin_inf());
           gpw(pr.C)[(size_t)i + (size_t)(c0 + jl) * pr.ldc] = from_dot(alpha, beta, d, cv[q]);
-          const int wi = 4 * (4 * (jl >> 4) + (il >> 4)) + (il & 3);
-          const uint64_t bit = 1ull << (16 * ((il & 15) >> 2) + (jl & 15));
-          atomicAnd(reinterpret_cast<unsigned long long*>(&fl[wi]), ~(unsigned long long)bit);
         }
+    }
+    // clear the decided flags: lanes il, il + 4, il + 8, il + 12 share the flag word of their
+    // block row and quarter -- their 16-bit masks merged by two shuffles, one LDS and per word
+    {
+      const int wi = 4 * (4 * (jb >> 4) + (il >> 4)) + (il & 3);
+      uint64_t mk = (uint64_t)(dec & 0xffffu) << (16 * ((il & 15) >> 2));
+      mk |= __shfl_xor(mk, 4);
+      mk |= __shfl_xor(mk, 8);
+      if (((il >> 2) & 3) == 0 && mk) atomicAnd(reinterpret_cast<unsigned long long*>(&fl[wi]), ~(unsigned long long)mk);
     }
     lds_sync();
     count_flags(fl, &cnt[0]);
     lds_sync();
     total = cnt[0];
-    if (total == 0) return;   // workgroup-uniform
+    if (total == 0) {   // workgroup-uniform
+      publish(false);
+      return;
+    }
   }
-  if (form == kDotFormDense || (form == kDotFormAuto && total >= kDenseMin)) {
+  const bool autof = form == kDotFormAuto || form == kDotFormTile;
+  if (form == kDotFormDense || (autof && total >= kDenseMin)) {
+    publish(false);
     dense_dots(pr, r0, c0, fl, buf);
     return;
   }
-  if (form == kDotFormAuto && t < 64) {   // rows and columns of the flagged entries: word t covers rows 16 bi + 4 q + e, columns 16 bj + c
+  if (autof && t < 64) {   // rows and columns of the flagged entries: word t covers rows 16 bi + 4 q + e, columns 16 bj + c
     const uint64_t v = fl[t];
     const int bi = (t >> 2) & 3, bj = t >> 4, e = t & 3;
     unsigned long long rb = 0ull;
@@ -1027,7 +1076,20 @@ __global__ void __launch_bounds__(kThreads, 6) dots_kernel(const oz2_problem* __
   // workgroup-uniform: moved to scalar registers, and everything derived from them with them
   const unsigned long long rmask = uniform_u64(rcm[0]), cmask = uniform_u64(rcm[1]);
   const int nR = __popcll(rmask), nC = __popcll(cmask);
-  if (form == kDotFormAuto && nR * nC <= kCompactMax) {   // workgroup-uniform
+  if (autof && nR * nC <= kCompactMax) {   // workgroup-uniform
+    // dense crossings with enough chains go to the crossings pass, which runs the crossings of all
+    // deferred rows and columns of the problem as one GEMM on the matrix cores (needs the gather
+    // workspace AT)
+    const bool defer = form == kDotFormAuto && yds[pi].AT && total >= kBandMin && 2 * total >= nR * nC;
+    publish(defer);
+    if (defer) {
+      if (t == 0) {
+        unsigned long long* const X = reinterpret_cast<unsigned long long*>(yds[pi].X);
+        atomicOr(&X[r0 >> 6], rmask);
+        atomicOr(&X[((m + 63) >> 6) + (c0 >> 6)], cmask);
+      }
+      return;
+    }
     if (t < 64) {
       if ((rmask >> t) & 1ull) rmap[__popcll(rmask & ((1ull << t) - 1ull))] = (uint8_t)t;
       if ((cmask >> t) & 1ull) cmap[__popcll(cmask & ((1ull << t) - 1ull))] = (uint8_t)t;
@@ -1036,6 +1098,7 @@ __global__ void __launch_bounds__(kThreads, 6) dots_kernel(const oz2_problem* __
     compact_dots(pr, r0, c0, fl, rmap, cmap, nR, nC, buf);
     return;
   }
+  publish(false);
   const int j = c0 + 16 * w + (lane & 15);
   for (int bi = 0; bi < 4; ++bi) {   // wave w: the blocks (bi, w)
     const int i0 = r0 + 16 * bi + 4 * (lane >> 4);
@@ -1064,6 +1127,264 @@ __global__ void __launch_bounds__(kThreads, 6) dots_kernel(const oz2_problem* __
   if (L > 0) sparse_dots(pr, r0, c0, list, L, buf);   // L is workgroup-uniform
 }
 
+
+// ---------------------------------------------------------------- crossings pass of the dot products
+// The chains dots_kernel deferred: 64 x 64 tiles whose remaining flagged entries form dense
+// crossings of a few rows and columns leave exactly those flags in the global flag words (the
+// other tiles leave zeros) and add their rows and columns to the problem's crossings sets X (bit
+// words: ceil(m / 64) for the rows, then ceil(n / 64) for the columns, cleared by the
+// reconstruct).  The crossings of the two sets, R x C, then run as one small GEMM per problem on
+// the FP64 matrix cores: gather_kernel copies the rows of R row-major and compact (row x of R at
+// AT + x k), as each deferred chain would otherwise read its row of column-major A a line per
+// value, and cross_kernel computes 64 x 64 tiles of R x C, 16 x 16 blocks per MFMA.
+//
+// v_mfma_f64_16x16x4f64 adds its four products to each accumulator as four sequential IEEE fmas in
+// k order (c -> k0 -> k1 -> k2 -> k3, each rounded; signed zeros, subnormals and infinities
+// included), so a block's chains over k = 4 t + g, t = 0, 1, .. from a zero accumulator are bit for
+// bit the sequential fma chains in ascending k from 0 of the reference's fp64_dot
+// (src/ozaki2_numerics.cu:445-452); k past the problem's k pads A with +0 and B with -0, whose
+// product -0 leaves every accumulator unchanged (+0 + -0 = +0 and -0 + -0 = -0 included).
+// Crossings whose flag is set are stored, the others are computed and dropped.
+
+// Sum of v over the workgroup (every thread gets it); ws: 4 ints of LDS, free again on return.
+__device__ __forceinline__ int block_sum(int v, int* ws) {
+#pragma unroll
+  for (int o = 32; o; o >>= 1) v += __shfl_xor(v, o);
+  if ((threadIdx.x & 63) == 0) ws[threadIdx.x >> 6] = v;
+  lds_sync();
+  int s = 0;
+#pragma unroll
+  for (int x = 0; x < kThreads / 64; ++x) s += ws[x];
+  lds_sync();
+  return s;
+}
+
+// Positions lo .. lo + 63 of the set bits of the nw words at Xw (bit b of word w is position
+// 64 w + b, counted in ascending order) into map[0 .. 63]; ws: 4 ints of LDS.  Thread t takes the
+// words [t per, (t + 1) per): its count, the workgroup's exclusive prefix of the counts, then the
+// walk of its words' bits that fall in the window.  Free of races on map and ws on return.
+__device__ void select_bits(const GLOBAL uint64_t* __restrict__ Xw, int nw, int lo, int* map, int* ws) {
+  const int t = threadIdx.x, lane = t & 63;
+  const int per = (nw + kThreads - 1) / kThreads, w0 = min(nw, t * per), w1 = min(nw, w0 + per);
+  int c = 0;
+  for (int x = w0; x < w1; ++x) c += __popcll(Xw[x]);
+  int inc = c;   // inclusive prefix in the wave
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(inc, o);
+    if (lane >= o) inc += y;
+  }
+  if (lane == 63) ws[t >> 6] = inc;
+  lds_sync();
+  int pos = inc - c;
+#pragma unroll
+  for (int x = 0; x < kThreads / 64; ++x) pos += x < (t >> 6) ? ws[x] : 0;
+  for (int x = w0; x < w1 && pos < lo + 64; ++x) {
+    uint64_t v = Xw[x];
+    const int pc = __popcll(v);
+    if (pos + pc <= lo) {
+      pos += pc;
+      continue;
+    }
+    while (v) {
+      if (pos >= lo && pos < lo + 64) map[pos - lo] = 64 * x + __builtin_ctzll(v);
+      ++pos;
+      v &= v - 1;
+    }
+  }
+  lds_sync();
+}
+
+constexpr int kGK = 64;   // gather: k per round
+
+// One workgroup per 64-row band of a problem (the row words of X): the band's rows of R copied to
+// AT at their positions in R, kGK values of k per round -- every lane loads one row of the band at
+// consecutive addresses (16-row groups without a row of R skipped), then each wave writes a row's
+// kGK values contiguously.  Band 0 also stores |R| and |C| in X's last word.
+__global__ void __launch_bounds__(kThreads) gather_kernel(const oz2_problem* __restrict__ probs,
+                                                         const YDesc* __restrict__ yds, int gne, int gper) {
+  __shared__ double T[kGK][kRT + 1];   // [k][band row], padded
+  __shared__ int rl[kRT];
+  __shared__ int ws[kThreads / 64];
+  int pi, band;
+  grid_tile<2>(yds, gne, gper, pi, band);
+  const oz2_problem& pr = probs[pi];
+  const int N = pr.num_moduli, m = pr.m, n = pr.n, K = pr.k;
+  const int r0 = band * kRT;
+  // workgroup-uniform: invalid problems, alpha = 0, bands past the problem, no deferral possible
+  if (N < 1 || N > kMaxModuli || m <= 0 || n <= 0 || K <= 0 || r0 >= m || pr.alpha == 0.0) return;
+  if (!yds[pi].fla || !yds[pi].AT) return;
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int m64 = (m + 63) >> 6, n64 = (n + 63) >> 6;
+  GLOBAL uint64_t* const X = gpw(yds[pi].X);
+  if (band == 0) {
+    int cr = 0, cc = 0;
+    for (int x = t; x < m64; x += kThreads) cr += __popcll(X[x]);
+    for (int x = t; x < n64; x += kThreads) cc += __popcll(X[m64 + x]);
+    cr = block_sum(cr, ws);
+    cc = block_sum(cc, ws);
+    if (t == 0) X[m64 + n64] = (uint64_t)(uint32_t)cr | ((uint64_t)(uint32_t)cc << 32);
+  }
+  const uint64_t bits = X[band];
+  if (bits == 0ull) return;   // workgroup-uniform
+  int before = 0;   // rows of R in the bands before
+  for (int x = t; x < band; x += kThreads) before += __popcll(X[x]);
+  before = block_sum(before, ws);
+  const int nb = __popcll(bits);
+  if ((bits >> lane) & 1ull && w == 0) rl[__popcll(bits & ((1ull << lane) - 1ull))] = lane;
+  lds_sync();
+  const GLOBAL double* const A = gp(pr.A);
+  GLOBAL double* const AT = gpw(yds[pi].AT);
+  const size_t lda = (size_t)pr.lda;
+  const bool load = r0 + lane < m && ((bits >> (lane & ~15)) & 0xffffull) != 0ull;
+  for (int k0 = 0; k0 < K; k0 += kGK) {
+    if (load) {
+      double v[kGK / 4];
+#pragma unroll
+      for (int s2 = 0; s2 < kGK / 4; ++s2) {
+        const int kk = w + 4 * s2;
+        v[s2] = k0 + kk < K ? A[(size_t)(r0 + lane) + (size_t)(k0 + kk) * lda] : 0.0;
+      }
+#pragma unroll
+      for (int s2 = 0; s2 < kGK / 4; ++s2) T[w + 4 * s2][lane] = v[s2];
+    }
+    lds_sync();
+    for (int q = w; q < nb; q += kThreads / 64) {
+      if (k0 + lane < K) AT[(size_t)(before + q) * (size_t)K + (size_t)(k0 + lane)] = T[lane][rl[q]];
+    }
+    lds_sync();
+  }
+}
+
+constexpr int kXK = 32;        // k per staged chunk
+constexpr int kXS = kXK + 2;   // LDS doubles per staged row / column (padded)
+constexpr int kXLoads = 2 * kRT * kXK / kThreads;   // staging loads per thread and chunk
+typedef double v4d __attribute__((ext_vector_type(4)));
+
+// The 64 x 64 tiles (ti, tj) of R x C, a few workgroups per problem (yds[p].xn of them, in
+// proportion to its dot-pass tiles; tiles t = workgroup, + xn, ..): rows 64 ti .. of R (from AT)
+// and columns 64 tj .. of C (B's columns) staged through LDS in k-chunks of kXK, row / column slot
+// major, double-buffered with the next chunk's loads in registers while the matrix cores run; wave w
+// owns the 2 x 2 blocks of block rows 2 (w % 2) .. and block columns 2 (w / 2) .., its next k-step's
+// operands read from LDS while the current step's MFMAs run.
+__global__ void __launch_bounds__(kThreads, 2) cross_kernel(const oz2_problem* __restrict__ probs,
+                                                           const YDesc* __restrict__ yds, int gne, int gper) {
+  __shared__ __attribute__((aligned(16))) double xs[2][2 * kRT * kXS];   // [buffer][A slots | B slots]
+  __shared__ int rmap[kRT], cmap[kRT];
+  __shared__ int ws[kThreads / 64];
+  int pi, wi;
+  grid_tile<3>(yds, gne, gper, pi, wi);
+  const int P = gne == 0 ? (int)gridDim.x : yds[pi].xn;   // the problem's workgroups
+  const oz2_problem& pr = probs[pi];
+  const int N = pr.num_moduli, m = pr.m, n = pr.n, K = pr.k;
+  // workgroup-uniform: invalid problems, alpha = 0 (no dot product), nothing deferred
+  if (N < 1 || N > kMaxModuli || m <= 0 || n <= 0 || K <= 0 || pr.alpha == 0.0) return;
+  if (!yds[pi].fla || !yds[pi].AT) return;
+  const int m64 = (m + 63) >> 6, n64 = (n + 63) >> 6;
+  const GLOBAL uint64_t* const X = gp(yds[pi].X);
+  const uint64_t tot = X[m64 + n64];
+  const int nR = (int)(uint32_t)tot, nC = (int)(uint32_t)(tot >> 32);
+  const int ntr = (nR + kRT - 1) / kRT, ntiles = ntr * ((nC + kRT - 1) / kRT);
+  if (wi >= ntiles) return;   // workgroup-uniform
+  const int t = threadIdx.x, lane = t & 63;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+  const GLOBAL double* const B = gp(pr.B);
+  const size_t ldb = (size_t)pr.ldb;
+  const int mb = (m + 15) >> 4;
+  const GLOBAL uint64_t* const F = gp(yds[pi].F);
+  const double alpha = pr.alpha, beta = pr.beta;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int rb0 = 2 * (w & 1), cb0 = 2 * (w >> 1);
+  for (int tile = wi; tile < ntiles; tile += P) {   // workgroup-uniform
+    const int ti = tile % ntr, tj = tile / ntr;
+    select_bits(X, m64, kRT * ti, rmap, ws);
+    select_bits(X + m64, n64, kRT * tj, cmap, ws);
+    const int nr = min(kRT, nR - kRT * ti), nc = min(kRT, nC - kRT * tj);
+    const GLOBAL double* const AT = gp(yds[pi].AT) + (size_t)(kRT * ti) * (size_t)K;
+    // staging element x = t + kThreads s: slot x / kXK of A (x < kRT kXK) or of B, at k x % kXK
+    double v[kXLoads];
+    // (inlined: a staging array passed to an outlined lambda by reference would live in scratch)
+    auto fetch = [&](int kc) __attribute__((always_inline)) {
+#pragma unroll
+      for (int s = 0; s < kXLoads; ++s) {
+        const int x = t + kThreads * s, slot = (x / kXK) % kRT, kk = x % kXK, k = kc + kk;
+        if (x < kRT * kXK)
+          v[s] = (slot < nr && k < K) ? AT[(size_t)slot * (size_t)K + (size_t)k] : 0.0;
+        else
+          v[s] = (slot < nc && k < K) ? B[(size_t)k + (size_t)cmap[slot] * ldb] : -0.0;
+      }
+    };
+    auto put = [&](double* dst) __attribute__((always_inline)) {
+#pragma unroll
+      for (int s = 0; s < kXLoads; ++s) {
+        const int x = t + kThreads * s;
+        dst[(x / kXK) * kXS + x % kXK] = v[s];   // B's slots follow A's (x / kXK >= kRT)
+      }
+    };
+    // wave-uniform: the wave's blocks that hold rows of R / columns of C
+    const bool rowA = 16 * rb0 < nr, rowB = 16 * (rb0 + 1) < nr;
+    const bool colA = 16 * cb0 < nc, colB = 16 * (cb0 + 1) < nc;
+    v4d acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[i][j] = v4d{0.0, 0.0, 0.0, 0.0};
+    fetch(0);
+    put(xs[0]);
+    if (kXK < K) fetch(kXK);
+    lds_sync();
+    int cur = 0;
+    for (int kc = 0; kc < K; kc += kXK) {
+      const int steps = (min(kXK, K - kc) + 3) >> 2;   // k-steps of 4 (the last padded)
+      if (rowA && colA) {
+        const double* const As = xs[cur] + (16 * rb0 + r16) * kXS + g;
+        const double* const Bs = xs[cur] + (kRT + 16 * cb0 + r16) * kXS + g;
+        double a0 = As[0], a1 = As[16 * kXS], b0 = Bs[0], b1 = Bs[16 * kXS];
+        for (int st = 0; st < steps; ++st) {
+          const int nx = 4 * min(st + 1, steps - 1);   // the next step's operands (the last reads its own)
+          const double na0 = As[nx], na1 = As[16 * kXS + nx], nb0 = Bs[nx], nb1 = Bs[16 * kXS + nx];
+          acc[0][0] = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b0, acc[0][0], 0, 0, 0);
+          if (colB) acc[0][1] = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b1, acc[0][1], 0, 0, 0);
+          if (rowB) acc[1][0] = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b0, acc[1][0], 0, 0, 0);
+          if (rowB && colB) acc[1][1] = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b1, acc[1][1], 0, 0, 0);
+          a0 = na0;
+          a1 = na1;
+          b0 = nb0;
+          b1 = nb1;
+        }
+      }
+      if (kc + kXK < K) {
+        put(xs[cur ^ 1]);   // chunk kc + kXK (the other buffer's last readers passed a barrier)
+        if (kc + 2 * kXK < K) fetch(kc + 2 * kXK);
+      }
+      lds_sync();   // chunk kc's steps done, chunk kc + kXK staged
+      cur ^= 1;
+    }
+    // accumulator element e of lane l: block row l / 16 + 4 e, block column l % 16
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int cs = 16 * (cb0 + j) + r16;
+        if (cs >= nc) continue;
+        const int col = cmap[cs];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int rs = 16 * (rb0 + i) + g + 4 * e;
+          if (rs >= nr) continue;
+          const int row = rmap[rs];
+          const uint64_t wv = F[4 * ((size_t)(col >> 4) * mb + (row >> 4)) + (row & 3)];
+          if ((wv >> (16 * ((row & 15) >> 2) + (col & 15))) & 1ull) {
+            const double d = e == 0 ? acc[i][j].x : (e == 1 ? acc[i][j].y : (e == 2 ? acc[i][j].z : acc[i][j].w));
+            GLOBAL double* cp = gpw(pr.C) + (size_t)row + (size_t)col * pr.ldc;
+            *cp = from_dot(alpha, beta, d, beta != 0.0 ? *cp : 0.0);
+          }
+        }
+      }
+    lds_sync();   // rmap / cmap and the staging are free for the next tile
+  }
+}
+
 }  // namespace
 
 int recon_launch(const oz2_problem* d, const YDesc* yd, int num, int max_m, int max_n, hipStream_t s, int mode,
@@ -1085,9 +1406,11 @@ int recon_launch(const oz2_problem* d, const YDesc* yd, int num, int max_m, int 
   // (a problem with fewer tiles returns from the surplus workgroups)
   const size_t gx = compact ? (size_t)grid->tiles : (size_t)((max_m + tm - 1) / tm) * (size_t)((max_n + tn - 1) / tn);
   const size_t gd = compact ? (size_t)grid->dtiles : (size_t)((max_m + kRT - 1) / kRT) * (size_t)((max_n + kRT - 1) / kRT);
-  if (gx > 0x7fffffffu || gd > 0x7fffffffu) return 1;
+  const size_t gb = compact ? (size_t)grid->bands : (size_t)((max_m + kRT - 1) / kRT);
+  if (gx > 0x7fffffffu || gd > 0x7fffffffu || gb > 0x7fffffffu) return 1;
   const unsigned gy = compact ? 1u : (unsigned)num;
   const int gne = compact ? num : 0, gper = compact ? grid->per : 0, dper = compact ? grid->dper : 0;
+  const int bper = compact ? grid->bper : 0;
   int nl = 0;
   if (gx > 0) {
     if (blk)
@@ -1104,6 +1427,13 @@ int recon_launch(const oz2_problem* d, const YDesc* yd, int num, int max_m, int 
   if (blk && gd > 0) {
     hipLaunchKernelGGL(dots_kernel, dim3((unsigned)gd, gy), dim3(kThreads), 0, s, d, yd, gne, dper, dot_form);
     ++nl;
+  }
+  // crossings workgroups: the compact grid's, else 64 per problem
+  const size_t gc = compact ? (size_t)grid->xwgs : (size_t)std::min<size_t>(gd, 64);
+  if (blk && gb > 0 && gc > 0) {   // the deferred chains: rows gathered, then the crossings
+    hipLaunchKernelGGL(gather_kernel, dim3((unsigned)gb, gy), dim3(kThreads), 0, s, d, yd, gne, bper);
+    hipLaunchKernelGGL(cross_kernel, dim3((unsigned)gc, gy), dim3(kThreads), 0, s, d, yd, gne, compact ? grid->xper : 0);
+    nl += 2;
   }
   if (launches) *launches = nl;
   return hipGetLastError() == hipSuccess ? 0 : 3;

@@ -296,7 +296,7 @@ def test_large_config_plan_execute_pointer_updates_sampled_bitwise():
                     st = G.Stats()
                     assert G.lib().ggemm_plan_get_stats(plan, C.byref(st)) == 0
                     oplan = oracle_plan(shapes, cfg, G.PATH_EMU_GROUPED)
-                    assert (st.num_fallback, st.moduli_min, st.moduli_max, st.kernel_launches) == (0, 16, 16, 4)
+                    assert (st.num_fallback, st.moduli_min, st.moduli_max, st.kernel_launches) == (0, 16, 16, 6)
                     assert all(e.route == 0 and e.num_moduli == 16 for e in oplan)
                     for (data, out, tag) in ((X, C1, "X -> C1"), (Y, C2, "Y -> C2"), (X, C2, "X -> C2")):
                         if tag != "X -> C1":

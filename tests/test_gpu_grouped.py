@@ -111,7 +111,9 @@ def device_model():
 # kernels of one emulated group call besides prep and the INT8 GEMM: the reconstruct, plus the
 # dot-product pass with the blocked digit layout (the default; GGEMM_DIGITS_COLMAJOR=1 turns it off)
 def recon_launches(blocked=True):
-    return 2 if blocked else 1
+    """Kernels of the reconstruct stage: the reconstruct, and with blocked digits the dot-product
+    pass, the gather of the crossings rows and the crossings pass."""
+    return 4 if blocked else 1
 
 
 def check_case(case, path, cfg, st, mode, blocked=True):
@@ -494,6 +496,61 @@ def test_dense_and_sparse_dot_forms(k, chains, form):
         assert rc == 0
         tot = check_case(case, G.PATH_EMU_GROUPED, cfg, st, O.REPAIR_ON if mode == G.REPAIR_ON else O.REPAIR_COUNT)
         assert tot[3] > 0
+
+
+@pytest.mark.parametrize("k", [3, 150, 1030])
+def test_repair_subgrid_dot_pass(k):
+    """Repairs concentrated in a sparse finite sub-grid (the hard config's pattern at reduced size):
+    most rows of A and columns of B hold a NaN / Inf and phi = 4 leaves most finite-row x
+    finite-column entries uncertified, so the dot pass decides the safety entries from the
+    summaries and runs the repairs' chains in the compact form over a tile's few rows and columns.
+    Tiles whose crossings are dense defer them to the crossings pass (regions of 2 x 16 tiles, the
+    chains in 16 x 16 blocks on the FP64 matrix cores).  ON and COUNT bitwise against the oracle
+    with the oracle's counts, and the same bits from a handle whose tiles never defer
+    (GGEMM_DOT_FORM=tile).  Shapes: several tiles and regions with short last ones (m = 300, 130),
+    a single tile row over 520 and 4200 columns (5 regions), repair rows in half the rows of one tile
+    row (m = 64, 1200 columns), and exactly 9 finite rows and 28 finite columns in every tile
+    (m = 128, n = 1100: 18 rows x 448 columns of crossings in the first region, 2 x 28 blocks in two
+    passes); k below a k-chunk, k % 4 != 0, alpha != 1, beta != 0."""
+    shapes = [(300, 280, k, -1.5, 0.5), (130, 300, k, 1.0, 0.0), (64, 520, k, 2.0, 1.0), (70, 4200, 40, 1.0, 0.0),
+              (64, 1200, 60, 1.0, 0.25), (128, 1100, k, 0.5, 0.0)]
+    # rows, columns with NaN / Inf: a rate, or exactly all but (9, 28) per 64-row / 64-column tile
+    rates = [(0.85, 0.85), (0.85, 0.85), (0.85, 0.85), (0.85, 0.85), (0.5, 0.875), (9, 28)]
+    case = Case(shapes, 20261251 + k, phi=4.0)
+    rng = np.random.default_rng(k + 7)
+    bad = [np.nan, np.inf, -np.inf]
+
+    def nonfinite(count, rate):
+        if isinstance(rate, float):
+            return [x for x in range(count) if rng.random() < rate]
+        keep = set()
+        for t0 in range(0, count, 64):
+            w = min(64, count - t0)
+            keep.update((t0 + rng.choice(w, min(rate, w), replace=False)).tolist())
+        return [x for x in range(count) if x not in keep]
+
+    for h, (rr, cr) in zip(case.hp, rates):
+        for i in nonfinite(h.m, rr):
+            h.A[i + int(rng.integers(0, h.k)) * h.lda] = bad[i % 3]
+        for j in nonfinite(h.n, cr):
+            h.B[int(rng.integers(0, h.k)) + j * h.ldb] = bad[j % 3]
+    case.alloc()
+    for mode in (G.REPAIR_ON, G.REPAIR_COUNT):
+        cfg = G.Config(0, 1e-15, 1, mode)
+        outs = []
+        for form in ("auto", "tile"):
+            say(f"repair sub-grid k={k} mode={mode} form={form}")
+            env = {} if form == "auto" else {"GGEMM_DOT_FORM": "tile"}
+            with env_handle(case, min_k=1, **env) as hd:
+                rc, st = run(case, G.PATH_EMU_GROUPED, cfg, handle=hd)
+            assert rc == 0
+            tot = check_case(case, G.PATH_EMU_GROUPED, cfg, st, O.REPAIR_ON if mode == G.REPAIR_ON else O.REPAIR_COUNT)
+            if mode == G.REPAIR_ON:
+                assert tot[2] > 1000, tot
+            outs.append([case.C(g).copy() for g in range(len(case.hp))])
+        for other in outs[1:]:
+            for a, b in zip(outs[0], other):
+                assert same_bits(a, b)
 
 
 def _inf_patterns(seed):

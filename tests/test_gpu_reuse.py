@@ -92,7 +92,7 @@ def test_reuse_matches_grouped_and_oracle(wl):
     assert (sb.reuse_enabled, sr.reuse_enabled, sa.reuse_enabled) == (0, 1, 0)
     assert (sb.num_unique_A, sb.num_unique_B) == (w.G, w.G)
     assert (sr.num_unique_A, sr.num_unique_B) == w.expect
-    assert sr.kernel_launches == sb.kernel_launches == 4
+    assert sr.kernel_launches == sb.kernel_launches == 6
     assert sr.num_promoted == 0
     assert (sr.num_uncertified, sr.num_repaired, sr.num_safety_fallback) == \
            (sb.num_uncertified, sb.num_repaired, sb.num_safety_fallback)
