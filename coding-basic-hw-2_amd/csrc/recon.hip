@@ -1385,6 +1385,22 @@ __global__ void __launch_bounds__(kThreads, 2) cross_kernel(const oz2_problem* _
   }
 }
 
+// Kernel of oz2_mfma_f64_chains: the accumulation the crossings pass relies on, for the tests.
+__global__ void __launch_bounds__(64) mfma_chain_kernel(const double* __restrict__ A, const double* __restrict__ B,
+                                                        double* __restrict__ D, int steps) {
+  const int w = blockIdx.x, l = threadIdx.x;
+  v4d acc = v4d{0.0, 0.0, 0.0, 0.0};
+  for (int t = 0; t < steps; ++t) {
+    const size_t x = ((size_t)w * steps + t) * 64 + l;
+    acc = __builtin_amdgcn_mfma_f64_16x16x4f64(A[x], B[x], acc, 0, 0, 0);
+  }
+  double* d = D + 256 * (size_t)w + 4 * l;
+  d[0] = acc.x;
+  d[1] = acc.y;
+  d[2] = acc.z;
+  d[3] = acc.w;
+}
+
 }  // namespace
 
 int recon_launch(const oz2_problem* d, const YDesc* yd, int num, int max_m, int max_n, hipStream_t s, int mode,
@@ -1440,6 +1456,13 @@ int recon_launch(const oz2_problem* d, const YDesc* yd, int num, int max_m, int 
 }
 
 }  // namespace ggemm
+
+extern "C" int oz2_mfma_f64_chains(const double* A, const double* B, double* D, int waves, int steps, hipStream_t s) {
+  if (waves < 1 || steps < 1) return 1;
+  hipLaunchKernelGGL(ggemm::mfma_chain_kernel, dim3((unsigned)waves), dim3(64), 0, s, A, B, D, steps);
+  if (hipGetLastError() != hipSuccess || hipStreamSynchronize(s) != hipSuccess) return 3;
+  return 0;
+}
 
 extern "C" int oz2_reconstruct_grouped(const oz2_problem* d, int num, int max_m, int max_n, hipStream_t s,
                                        int repair_mode) {

@@ -128,6 +128,7 @@ SIGNATURES = [
     ("oz2_choose_num_moduli_cw", C.c_int, [C.c_int, C.c_double]),
     ("oz2_read_counters", C.c_int, [C.POINTER(Oz2Counters), C.c_int, _P]),
     ("oz2_debug_force_prep_split", None, [C.c_int]),
+    ("oz2_mfma_f64_chains", C.c_int, [_P, _P, _P, C.c_int, C.c_int, _P]),
     ("i8_grouped_gemm_sched_ws_bytes", C.c_size_t, [C.c_int, C.c_size_t]),
     ("i8_grouped_gemm_reserve", None, [C.c_int, C.c_size_t]),
     ("i8_grouped_gemm_host_allocs", C.c_longlong, []),

@@ -31,8 +31,9 @@ typedef enum {
   GGEMM_PATH_NATIVE_LOOP = 0,        /* native FP64 (own FP64-MFMA DGEMM), one launch per problem */
   GGEMM_PATH_NATIVE_GROUPED = 1,     /* native FP64, one grouped launch */
   GGEMM_PATH_EMU_LOOP = 2,           /* per problem: prep, one INT8 GEMM per plane, reconstruct */
-  GGEMM_PATH_EMU_GROUPED = 3,        /* fused grouped pipeline: 4 launches for the whole group
-                                        (prep, INT8 GEMM, reconstruct, FP64 dot-product pass) */
+  GGEMM_PATH_EMU_GROUPED = 3,        /* fused grouped pipeline: 6 launches for the whole group
+                                        (prep, INT8 GEMM, reconstruct, FP64 dot-product pass, the
+                                        pass's row gather and crossings GEMM) */
   GGEMM_PATH_AUTO = 4,               /* EMU_GROUPED + planner (adaptive N, cost-based fallback) */
   GGEMM_PATH_EMU_GROUPED_REUSE = 5,  /* EMU_GROUPED + operand reuse */
   GGEMM_PATH_EMU_LOOP_BATCHED = 6    /* per problem: prep, one INT8 GEMM over its planes, reconstruct */

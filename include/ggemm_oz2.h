@@ -67,6 +67,13 @@ typedef struct {
 int oz2_read_counters(oz2_counters* out, int reset, hipStream_t s);
 /* src/ozaki2_numerics.h:105: force the prep K-split factor (1..64, 0 = automatic). */
 void oz2_debug_force_prep_split(int S);
+/* No counterpart in the reference: the FP64 matrix-core chains the dot pass's crossings rely on, for
+   the tests.  Wave w (64 lanes, one workgroup each) runs steps t = 0 .. steps - 1 of
+   v_mfma_f64_16x16x4f64 from a zero accumulator on A[(w steps + t) 64 + l], B[(w steps + t) 64 + l]
+   (lane l holds row / column l % 16 at k = 4 t + l / 16) and stores element e of lane l at
+   D[256 w + 4 l + e] (output row l / 16 + 4 e, column l % 16).  Device pointers; one launch,
+   synchronous.  Returns 0, or 1 for waves < 1 or steps < 1, 3 for a launch error. */
+int oz2_mfma_f64_chains(const double* A, const double* B, double* D, int waves, int steps, hipStream_t s);
 
 /* ------------------------------------------------------------------ INT8 grouped GEMM */
 /* src/int8_grouped_gemm.h:16-23.  C = A * B^T: C[i + j*m] = sum_k A[i*kp + k] * B[j*kp + k]. */

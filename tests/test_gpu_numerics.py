@@ -4,6 +4,7 @@ and the reference's logged known answers (tests/test_numerics_standalone.cu sect
 Bar: residue planes, shifts and norm bounds bit-exact; INT8 products bit-exact; reconstructed C
 bit-identical to the oracle; repaired / uncertified / safety / non-finite counts equal to the
 oracle's and to the reference log."""
+import ctypes as C
 import json
 from pathlib import Path
 
@@ -198,3 +199,74 @@ def test_prep_split_invariance():
     finally:
         G.lib().oz2_debug_force_prep_split(0)
         read_counters()
+
+
+def _chain_operands(rng, kind, waves, K):
+    """Per wave a 16 x K block of A and a K x 16 block of B (column-major) of one input class."""
+    def wide(shape, lo, hi):
+        v = np.ldexp(rng.uniform(1.0, 2.0, shape), rng.integers(lo, hi + 1, shape))
+        return np.where(rng.random(shape) < 0.5, -v, v)
+
+    A = wide((waves, K, 16), -60, 60)   # [w][k][i]
+    B = wide((waves, 16, K), -60, 60)   # [w][j][k]
+    if kind == "cancellation":          # each chain's later products undo its first one's rounding
+        A = wide((waves, K, 16), -2, 2)
+        B = wide((waves, 16, K), -2, 2)
+        A[:, 1::2, :] = -A[:, 0::2, :] * (1.0 + np.ldexp(rng.integers(-3, 4, A[:, 1::2, :].shape), -52))
+        A[:, 2::4, :] = np.ldexp(A[:, 2::4, :], -rng.integers(20, 60, A[:, 2::4, :].shape))
+    elif kind == "subnormal":
+        A = wide((waves, K, 16), -540, -500)
+        B = wide((waves, 16, K), -540, -500)
+    elif kind == "zeros":               # signed zeros and products that underflow to -0 / +0
+        A = wide((waves, K, 16), -560, -520)
+        B = wide((waves, 16, K), -540, -500)
+        A = np.where(rng.random(A.shape) < 0.25, np.where(rng.random(A.shape) < 0.5, -0.0, 0.0), A)
+        B = np.where(rng.random(B.shape) < 0.25, np.where(rng.random(B.shape) < 0.5, -0.0, 0.0), B)
+    elif kind == "overflow":            # +-Inf and NaN factors, sums past the largest double
+        A = wide((waves, K, 16), 500, 512)
+        B = wide((waves, 16, K), 500, 512)
+        r = rng.integers(0, 16, A.shape)
+        A = np.where(r == 0, np.inf, np.where(r == 1, -np.inf, np.where(r == 2, np.nan, A)))
+    return A, B
+
+
+@pytest.mark.parametrize("kind", ["wide", "cancellation", "subnormal", "zeros", "overflow"])
+@pytest.mark.parametrize("steps", [1, 3, 64])
+def test_fp64_mfma_chains_are_sequential_fmas(kind, steps):
+    """The dot pass's crossings pass computes repair chains with v_mfma_f64_16x16x4f64: its four
+    k-steps must be four sequential IEEE fmas in k order, so that a block's chains equal the
+    oracle's fp64_dot (one fma chain in ascending k from +0) bit for bit.  Inputs that tell the
+    orders apart (one rounding of the exact sum, or k descending, differ from the chain in a
+    large share of these cases): wide exponents, cancellation, subnormal products, signed zeros
+    and underflow to zero, infinities and NaN with overflowing sums; k = 4, 12, 256."""
+    rng = np.random.default_rng(20261202 + steps + 100 * len(kind))
+    waves, K = 64, 4 * steps
+    A, B = _chain_operands(rng, kind, waves, K)
+    # lane l of step t holds A[i = l % 16][k = 4 t + l / 16] and B[k][j = l % 16]
+    l = np.arange(64)
+    kk = 4 * np.arange(steps)[:, None] + (l // 16)[None, :]               # [t][l]
+    Al = A[:, kk, (l % 16)[None, :]]                                      # [w][t][l]
+    Bl = B[:, (l % 16)[None, :], kk]
+    dA = torch.from_numpy(np.ascontiguousarray(Al)).cuda()
+    dB = torch.from_numpy(np.ascontiguousarray(Bl)).cuda()
+    dD = torch.full((waves * 256,), 7.0, dtype=torch.float64, device="cuda")
+    say(f"mfma chains {kind} steps={steps}")
+    assert G.lib().oz2_mfma_f64_chains(dA.data_ptr(), dB.data_ptr(), dD.data_ptr(), waves, steps, None) == 0
+    D = dD.cpu().numpy().reshape(waves, 64, 4)
+    lib = O.oracle()
+    want = np.empty_like(D)
+    alt = 0
+    for w in range(waves):
+        Aw = np.ascontiguousarray(A[w])          # [k][i]: row i at Aw + i with stride 16
+        Bw = np.ascontiguousarray(B[w])          # [j][k]: column j contiguous
+        for ln in range(64):
+            for e in range(4):
+                i, j = ln // 16 + 4 * e, ln % 16
+                want[w, ln, e] = lib.oz2o_fp64_dot(K, C.c_void_p(Aw[:, i:].ctypes.data), 16,
+                                                   C.c_void_p(Bw[j].ctypes.data))
+                with np.errstate(all="ignore"):   # another order: must differ sometimes
+                    exact = float(np.sum(Aw[:, i] * Bw[j]))
+                alt += not same_bits(exact, want[w, ln, e])
+    assert same_bits(D, want), f"{kind}: {np.sum(~((D == want) | (np.isnan(D) & np.isnan(want))))} chains differ"
+    if steps > 1 and kind in ("wide", "cancellation", "subnormal"):
+        assert alt > 0, "the inputs do not tell the summation orders apart"
