@@ -310,27 +310,31 @@ def main():
     # finite column (their entries all take the safety fallback): the roofline counts the
     # operations of the computed tiles (large-tile kernel: 256 x 256 tiles, checked when kp > 192)
     computed_ops, skipped_share = int8_ops, 0.0
+    fin = {g: (shapes[g][0], shapes[g][1]) for g in emu}   # finite rows of A, finite columns of B
     if bad > 0.0 and emu:
+        computed_ops = 0.0
+        for g in emu:
+            m, n, k = shapes[g][:3]
+            kp = kp_of(k)
+            rf = torch.isfinite(A[g]).all(dim=0).view(-1)   # rows of A (torch (k, m))
+            cf = torch.isfinite(B[g]).all(dim=1).view(-1)   # columns of B (torch (n, k))
+            fin[g] = (int(rf.sum().item()), int(cf.sum().item()))
+            tr = torch.nn.functional.pad(rf, (0, (-m) % 256)).view(-1, 256).any(dim=1)
+            tc = torch.nn.functional.pad(cf, (0, (-n) % 256)).view(-1, 256).any(dim=1)
+            live = int((tr[:, None] & tc[None, :]).sum().item()) if kp > 192 else tr.numel() * tc.numel()
+            computed_ops += (plan_e[g].num_moduli + 1) * 2.0 * m * n * kp * live / (tr.numel() * tc.numel())
+        skipped_share = 1.0 - computed_ops / int8_ops
         if i8_kernel != "i8_large_kernel":
-            computed_ops = None   # tile shapes per product are the schedule's choice: not counted here
-        else:
-            computed_ops = 0.0
-            for g in emu:
-                m, n, k = shapes[g][:3]
-                kp = kp_of(k)
-                rf = torch.isfinite(A[g]).all(dim=0).view(-1)   # rows of A (torch (k, m))
-                cf = torch.isfinite(B[g]).all(dim=1).view(-1)   # columns of B (torch (n, k))
-                tr = torch.nn.functional.pad(rf, (0, (-m) % 256)).view(-1, 256).any(dim=1)
-                tc = torch.nn.functional.pad(cf, (0, (-n) % 256)).view(-1, 256).any(dim=1)
-                live = int((tr[:, None] & tc[None, :]).sum().item()) if kp > 192 else tr.numel() * tc.numel()
-                computed_ops += (plan_e[g].num_moduli + 1) * 2.0 * m * n * kp * live / (tr.numel() * tc.numel())
-            skipped_share = 1.0 - computed_ops / int8_ops
+            computed_ops, skipped_share = None, 0.0   # tile shapes per product are the schedule's choice
     achieved = computed_ops / (i8_ms * 1e-3) / 1e12 if computed_ops and i8_ms > 0 else None
+    # prep: reads A and B once; residue planes only for the finite rows / columns (the others get
+    # none), shifts for all
     prep_bytes = sum(8.0 * (shapes[g][0] * shapes[g][2] + shapes[g][1] * shapes[g][2]) +
-                     (plan_e[g].num_moduli + 1) * (shapes[g][0] + shapes[g][1]) * kp_of(shapes[g][2]) +
+                     (plan_e[g].num_moduli + 1) * (fin[g][0] + fin[g][1]) * kp_of(shapes[g][2]) +
                      16.0 * (shapes[g][0] + shapes[g][1]) for g in emu)
-    # reconstruct: N digit bytes + the int32 abs-plane product per entry, C0 (beta != 0), C, shifts
-    recon_bytes = sum((plan_e[g].num_moduli + 4.0) * shapes[g][0] * shapes[g][1] +
+    # reconstruct: N digit bytes + the int32 abs-plane product per entry of a finite row and column
+    # (the others read no digits), C0 (beta != 0), C, shifts
+    recon_bytes = sum((plan_e[g].num_moduli + 4.0) * fin[g][0] * fin[g][1] +
                       8.0 * shapes[g][0] * shapes[g][1] * (2 if shapes[g][4] != 0 else 1) +
                       16.0 * (shapes[g][0] + shapes[g][1]) for g in emu)
 
