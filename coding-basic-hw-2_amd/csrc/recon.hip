@@ -1256,7 +1256,7 @@ __global__ void __launch_bounds__(kThreads) gather_kernel(const oz2_problem* __r
   }
 }
 
-constexpr int kXK = 32;        // k per staged chunk
+constexpr int kXK = 16;        // k per staged chunk
 constexpr int kXS = kXK + 2;   // LDS doubles per staged row / column (padded)
 constexpr int kXLoads = 2 * kRT * kXK / kThreads;   // staging loads per thread and chunk
 typedef double v4d __attribute__((ext_vector_type(4)));
@@ -1267,7 +1267,7 @@ typedef double v4d __attribute__((ext_vector_type(4)));
 // major, double-buffered with the next chunk's loads in registers while the matrix cores run; wave w
 // owns the 2 x 2 blocks of block rows 2 (w % 2) .. and block columns 2 (w / 2) .., its next k-step's
 // operands read from LDS while the current step's MFMAs run.
-__global__ void __launch_bounds__(kThreads, 2) cross_kernel(const oz2_problem* __restrict__ probs,
+__global__ void __launch_bounds__(kThreads, 4) cross_kernel(const oz2_problem* __restrict__ probs,
                                                            const YDesc* __restrict__ yds, int gne, int gper) {
   __shared__ __attribute__((aligned(16))) double xs[2][2 * kRT * kXS];   // [buffer][A slots | B slots]
   __shared__ int rmap[kRT], cmap[kRT];
