@@ -130,11 +130,16 @@ __host__ __device__ inline size_t packed_offset(int row, int k, int rows, int kp
 // row_shift, col_shift) and its non-finite flag (YDesc::nff).  When prep has set the flag, a tile
 // whose rows, or whose columns, all carry OZ2_SHIFT_NONFINITE is not computed: each of its entries
 // takes the safety fallback, which uses none of the tile's outputs.
+struct YDesc;
 struct I8Epi {
   uint32_t mode, p, mc, bias;
   const int32_t* rs;
   const int32_t* cs;
   const int* nf;
+  // the product's reconstruct descriptor (blocked grouped calls, nullptr otherwise): with its
+  // non-finite flag set, the dispatched INT8 kernels compute only the finite rows x finite columns
+  // (its finite-row / finite-column lists, below), each tile over consecutive entries of the lists
+  const YDesc* yd;
 };
 I8Epi i8_epi_residue(uint32_t p, int kp);
 __host__ __device__ inline size_t blocked_plane_entries(int m, int n) {
@@ -202,6 +207,10 @@ struct YDesc {
   // the residue workspace (free once the INT8 GEMM is done), nullptr: the dot pass defers nothing
   uint64_t* X;
   double* AT;
+  // finite rows of A / columns of B (blocked layout): fr[i], fc[j] 1 for a finite row / column, 0
+  // else, written by prep every call; each list starts 4-byte aligned (fc at fr + m rounded up to 4)
+  uint8_t* fr;
+  uint8_t* fc;
   int t0, d0, b0, x0;   // the problem's first workgroup in the reconstruct, dot-pass, row-band and
                         // crossings grids
   int xn;               // the problem's crossings workgroups
@@ -216,9 +225,11 @@ struct ReconGrid {
 // Reconstruct tile shapes (rows x columns per workgroup): blocked digits / column-major, and the
 // dot-product pass's tile
 constexpr int kReconTileMB = 64, kReconTileNB = 16, kReconTileMC = 128, kReconTileNC = 8, kDotTile = 64;
-// Bytes of a problem's flags plus its crossings sets (blocked layout)
+// Bytes of a problem's flags plus its crossings sets and finite-row / finite-column bytes (blocked
+// layout)
 inline size_t flag_bytes(int m, int n, size_t plane_entries) {
-  return plane_entries / 8 + sizeof(uint64_t) * (size_t)((m + 63) / 64 + (n + 63) / 64 + 1);
+  return plane_entries / 8 + sizeof(uint64_t) * (size_t)((m + 63) / 64 + (n + 63) / 64 + 1) +
+         (((size_t)m + 3) & ~(size_t)3) + (((size_t)n + 3) & ~(size_t)3);
 }
 // Prep workgroup shapes: rows of A per A-row block, columns of B per B-column block
 constexpr int kPrepRows = 32, kPrepCols = 8;
@@ -306,4 +317,5 @@ struct ggemm_handle_s {
   int safety_chains;   // GGEMM_SAFETY_CHAINS=1 at create: safety-fallback entries always run their fma
                        // chains instead of being decided from prep's non-finite summaries (testing)
   int dot_form;        // GGEMM_DOT_FORM at create: kDotForm* (testing)
+  int compact;         // GGEMM_COMPACT at create (default 1; 0: INT8 tiles over all rows / columns, testing)
 };

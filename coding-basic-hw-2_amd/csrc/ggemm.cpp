@@ -305,6 +305,8 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
     yd.F = c.blocked ? reinterpret_cast<uint64_t*>(fbase + of) : nullptr;
     yd.nf = nfsum ? reinterpret_cast<int32_t*>(nbase + onf) : nullptr;
     yd.X = c.blocked ? reinterpret_cast<uint64_t*>(fbase + of + blocked_plane_entries(p.m, p.n) / 8) : nullptr;
+    yd.fr = c.blocked ? reinterpret_cast<uint8_t*>(yd.X + ((p.m + 63) / 64 + (p.n + 63) / 64 + 1)) : nullptr;
+    yd.fc = c.blocked ? yd.fr + (((size_t)p.m + 3) & ~(size_t)3) : nullptr;
     {   // the gather workspace: the problem's m k doubles in the residue planes, while they last
       const size_t at = align_up((size_t)p.m * (size_t)p.k * sizeof(double), kBufAlign);
       yd.AT = nullptr;
@@ -353,6 +355,9 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
       hepi[q].rs = o.row_shift;
       hepi[q].cs = o.col_shift;
       hepi[q].nf = reinterpret_cast<const int*>(db + c.L.off_yd + j * sizeof(YDesc) + offsetof(YDesc, nff));
+      // finite rows x finite columns only, for problems prep finds non-finite (its own residues)
+      hepi[q].yd = (c.blocked && !rp && h->compact) ? reinterpret_cast<const YDesc*>(db + c.L.off_yd + j * sizeof(YDesc))
+                                                    : nullptr;
     }
     const size_t plane = c.blocked ? blocked_plane_entries(p.m, p.n) : (size_t)p.m * p.n;
     oy += align_up(plane, kBufAlign);
@@ -842,6 +847,8 @@ extern "C" int ggemm_create_ex(ggemm_handle_t* out, int max_problems, size_t max
   h->packed_env = epk ? 1 : 0;
   const char* esf = std::getenv("GGEMM_SAFETY_CHAINS");
   h->safety_chains = (esf && std::atoi(esf) == 1) ? 1 : 0;
+  const char* ecp = std::getenv("GGEMM_COMPACT");
+  h->compact = (ecp && std::atoi(ecp) == 0) ? 0 : 1;
   const char* edf = std::getenv("GGEMM_DOT_FORM");
   h->dot_form = !edf                          ? kDotFormAuto
                 : !std::strcmp(edf, "dense")  ? kDotFormDense

@@ -232,6 +232,41 @@ __device__ __forceinline__ void dma_stage_full(const int8_t* a, const int8_t* b,
       });
 }
 
+// A stage of a compacted tile: the tile's rows are entries row0 .. of the product's finite-row list
+// and its columns entries col0 .. of its finite-column list (rm / cm: the tile's window of the lists
+// in LDS, nr / nc entries from row0 / col0 on; rows past a list repeat its last, and their results
+// are not stored), so each lane's row of each of its pieces is gathered; VM DMA instructions per
+// wave, selects rather than branches between them.
+template <class C, bool kPacked>
+__device__ __forceinline__ void dma_stage_mapped(const int8_t* A, const int8_t* B, int m, int n, int kp, int k0,
+                                                 const int* rm, const int* cm, int nr, int nc, uint8_t* st,
+                                                 int wave, int lane) {
+  const int r_in = lane / C::CH, pc = lane % C::CH;
+#pragma unroll
+  for (int q = 0; q < C::VM; ++q) {
+    const int g = wave + C::NW * q;
+    const bool isa = g < C::PA;
+    const int piece = isa ? g : g - C::PA;
+    const int row = piece * C::RP + r_in;
+    const int kk = 16 * swz<C::CH>(row, pc);
+    const int8_t* const plane = isa ? A : B;
+    const int rows = isa ? m : n, lr = isa ? nr : nc;
+    const int orow = (isa ? rm : cm)[row < lr ? row : lr - 1];
+    size_t off;
+    int lim;
+    if (kPacked) {
+      const int b = k0 >> 6, rb = b == (kp >> 6) ? 32 : 64;
+      off = (size_t)b * rows * 64 + (size_t)orow * rb;
+      lim = rb;
+    } else {
+      off = (size_t)orow * kp + k0;
+      lim = kp - k0;
+    }
+    __builtin_amdgcn_global_load_lds((const void*)(plane + off + (kk < lim ? kk : 0)),
+                                     GGEMM_LDS(st + (isa ? 0 : C::SA) + piece * 1024), 16, 0, 0);
+  }
+}
+
 // C mod p in [0, p) from u = C + bias >= 0: q = umulhi(u, mc) with mc = ceil(2^32 / p) is floor(u / p)
 // or one more (u (mc - 2^32/p) < 2^32), so r = u - q p is in [-p, p), and min(r, r + p) as unsigned
 // is r mod p.  kAcc: u is the accumulator (it started at the bias), u < 2^30 + p and q < 2^23, so
@@ -278,12 +313,40 @@ __device__ __forceinline__ void store_blocked(const v4i (&acc)[C::FM][C::FN], co
 }
 
 // Epilogue of a tile: the accumulators of the wave (wm, wn) = (wave % WGM, wave / WGM) stored as int32
-// or residue bytes, blocked or column-major (I8Epi).
+// or residue bytes, blocked or column-major (I8Epi).  Compacted tile (rmap != nullptr, blocked only):
+// tile row r is product row rmap[r] (r < nr), tile column c product column cmap[c] (c < nc), each
+// entry stored at its own place in the blocked layout.
 template <class C>
 __device__ __forceinline__ void tile_epilogue(const v4i (&acc)[C::FM][C::FN], const i8_problem& P, const I8Epi& epi,
-                                              int row0, int col0, int wave, int lane) {
+                                              int row0, int col0, int wave, int lane, const int* rmap = nullptr,
+                                              const int* cmap = nullptr, int nr = 0, int nc = 0) {
   constexpr int FM = C::FM, FN = C::FN;
   const int wm = wave % C::WGM, wn = wave / C::WGM;
+  if (rmap) {
+    const bool res = (epi.mode & kEpiResidue) != 0, accb = (epi.mode & kEpiAccBias) != 0;
+    const int mb = (P.m + 15) / 16;
+    GLOBAL uint8_t* const y8 = (GLOBAL uint8_t*)P.C;
+    GLOBAL int32_t* const y32 = (GLOBAL int32_t*)P.C;
+    static_for<0, FM * FN>([&](auto ij) {
+      constexpr int i = decltype(ij)::value / FN, j = decltype(ij)::value % FN;
+      const int cl = wn * C::WN + j * 16 + (lane & 15);
+      if (cl < nc) {
+        const int oc = cmap[cl];
+        const v4i v = acc[i][j];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int rl = wm * C::WM + i * 16 + 4 * (lane >> 4) + r;
+          if (rl < nr) {
+            const int orr = rmap[rl];
+            const size_t e = blocked_word(orr & ~3, oc, mb) + (size_t)(orr & 3);
+            if (!res) y32[e] = v[r];
+            else y8[e] = (uint8_t)(accb ? residue_byte<true>(v[r], epi) : residue_byte<false>(v[r], epi));
+          }
+        }
+      }
+    });
+    return;
+  }
   // D block layout: lane l, register r -> row 4 (l / 16) + r, column l % 16; a lane's 4 values
   // are 4 consecutive rows of one column, i.e. contiguous in the column-major output, and the
   // 64 lanes' values are one 16 x 16 block of the blocked output layout.
@@ -349,6 +412,21 @@ struct TileSrc {
   bool full_rows;
   uint32_t lane_off;
   int wave, lane;
+  // compacted tile (rm != nullptr): rows tm BM .. of the finite-row list (rm: the tile's window of
+  // it in LDS, nr = m_rem >= 1 entries from there on), columns tn BN .. of the finite-column list
+  const int* rm = nullptr;
+  const int* cm = nullptr;
+  __device__ __forceinline__ TileSrc(const i8_problem& P, int tm, int tn, const int* rmap, const int* cmap, int nr,
+                                     int nc)
+      : A(P.A), B(P.B), m(P.m), n(P.n), kp(P.kp), row0(tm * C::BM), col0(tn * C::BN), m_rem(nr), n_rem(nc) {
+    const int tid = tile_tid();
+    lane = tid & 63;
+    wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    full_rows = false;
+    lane_off = 0;
+    rm = rmap;
+    cm = cmap;
+  }
   __device__ __forceinline__ TileSrc(const i8_problem& P, int tm, int tn)
       : A(P.A), B(P.B), m(P.m), n(P.n), kp(P.kp), row0(tm * C::BM), col0(tn * C::BN), m_rem(P.m - tm * C::BM),
         n_rem(P.n - tn * C::BN) {
@@ -365,6 +443,10 @@ struct TileSrc {
   }
   __device__ __forceinline__ void load(int kt, uint8_t* st) const {
     const int k0 = kt * C::BK;
+    if (rm) {
+      dma_stage_mapped<C, kPacked>(A, B, m, n, kp, k0, rm, cm, m_rem, n_rem, st, wave, lane);
+      return;
+    }
     if (full_rows && k0 + C::BK <= kp) {
       const int8_t* a = kPacked ? A + (size_t)(k0 >> 6) * m * 64 + (size_t)row0 * 64 : A + (size_t)row0 * kp + k0;
       const int8_t* b = kPacked ? B + (size_t)(k0 >> 6) * n * 64 + (size_t)col0 * 64 : B + (size_t)col0 * kp + k0;
@@ -415,11 +497,12 @@ struct Unit {
 template <class C, bool kPacked, bool kFresh, class Claim, class Next>
 __device__ __forceinline__ bool run_tile(uint8_t* lds, const i8_problem* __restrict__ probs,
                                          const I8Epi* __restrict__ epis, int pi, int tm, int tn, Claim&& claim,
-                                         Next&& next) {
+                                         Next&& next, const int* rmap = nullptr, const int* cmap = nullptr,
+                                         int nr = 0, int nc = 0) {
   const i8_problem& P = probs[pi];
   const I8Epi epi = epi_of(epis, pi);
   constexpr int FM = C::FM, FN = C::FN, NST = C::NST;
-  const TileSrc<C, kPacked> src(P, tm, tn);
+  const TileSrc<C, kPacked> src = rmap ? TileSrc<C, kPacked>(P, tm, tn, rmap, cmap, nr, nc) : TileSrc<C, kPacked>(P, tm, tn);
   const int tid = tile_tid(), lane = tid & 63, wave = src.wave;
   const int wm = wave % C::WGM, wn = wave / C::WGM;
   const int kp = P.kp;
@@ -608,7 +691,7 @@ __device__ __forceinline__ bool run_tile(uint8_t* lds, const i8_problem* __restr
   // the epilogue's descriptor fields are read again here rather than kept live through the k loop
   int pi_e = pi;
   asm volatile("" : "+s"(pi_e));
-  tile_epilogue<C>(acc, probs[pi_e], epi_of(epis, pi_e), src.row0, src.col0, wave, lane);
+  tile_epilogue<C>(acc, probs[pi_e], epi_of(epis, pi_e), src.row0, src.col0, wave, lane, rmap, cmap, nr, nc);
   return prefetched;
 }
 
@@ -638,6 +721,13 @@ __device__ __forceinline__ void raster(int local, int m, int n, int bm, int bn, 
   const int r = local - g * per_group;
   tm = first_m + r % gsz;
   tn = r / gsz;
+}
+// the local index of tile (tm, tn) in raster<GM>'s order
+template <int GM>
+__device__ __forceinline__ int raster_local(int tm, int tn, int m, int n, int bm, int bn) {
+  const int tiles_m = (m + bm - 1) / bm, tiles_n = (n + bn - 1) / bn;
+  const int g = tm / GM, first_m = g * GM, gsz = min(GM, tiles_m - first_m);
+  return g * GM * tiles_n + tn * gsz + (tm - first_m);
 }
 // unit u (wave-uniform, >= 0) -> problem, tile configuration and tile position
 template <int GM, bool kLarge>
@@ -760,9 +850,121 @@ __device__ __forceinline__ int dispatched_unit(const int* __restrict__ sched) {
   const int x = b % kXcds, q = b / kXcds;
   return (q / CH) * span + x * CH + (q % CH);
 }
-// With the product's shifts given (epi.nf) and its non-finite flag set by prep, a tile whose rows
-// or whose columns are all non-finite is dropped: every entry of it takes the safety fallback.
-// Only on tiles of at least PRE stages.  Each wave DMAs 64 of the tile's row shifts and 64 of its
+// Finite-row / finite-column lists (bytes 0 / 1 in index order, 4-byte aligned, bytes past the
+// list's length ignored), read as words.
+__device__ __forceinline__ uint32_t flag_word(const uint32_t* __restrict__ fw, int total, int x) {
+  const int nb = total - 4 * x;
+  return nb >= 4 ? fw[x] : fw[x] & ((1u << (8 * nb)) - 1u);
+}
+__device__ __forceinline__ int flag_sum(uint32_t w) { return (int)((w * 0x01010101u) >> 24); }
+
+// The set flags of both lists counted by the workgroup; ws: 2 NT / 64 ints of LDS.  One barrier.
+template <int NT>
+__device__ __forceinline__ int2 count_lists(const uint8_t* __restrict__ fr, int m, const uint8_t* __restrict__ fc,
+                                            int n, int* ws) {
+  const int t = tile_tid(), lane = t & 63, w = t >> 6;
+  const uint32_t* __restrict__ rw = reinterpret_cast<const uint32_t*>(fr);
+  const uint32_t* __restrict__ cw = reinterpret_cast<const uint32_t*>(fc);
+  int cr = 0, cc = 0;
+  for (int x = t; x < (m + 3) >> 2; x += NT) cr += flag_sum(flag_word(rw, m, x));
+  for (int x = t; x < (n + 3) >> 2; x += NT) cc += flag_sum(flag_word(cw, n, x));
+#pragma unroll
+  for (int o = 32; o; o >>= 1) {
+    cr += __shfl_xor(cr, o);
+    cc += __shfl_xor(cc, o);
+  }
+  if (lane == 0) {
+    ws[2 * w] = cr;
+    ws[2 * w + 1] = cc;
+  }
+  __syncthreads();
+  int2 r = make_int2(0, 0);
+#pragma unroll
+  for (int q = 0; q < NT / 64; ++q) {
+    r.x += ws[2 * q];
+    r.y += ws[2 * q + 1];
+  }
+  return r;
+}
+
+// Entries lo .. lo + win - 1 of the list of the set flags f[0 .. total) into map[0 .. win) (as far
+// as the list goes); ws: NT / 64 ints of LDS.  Thread t takes words [t per, (t + 1) per): the
+// workgroup's exclusive prefix of their flag counts gives its first list position, and it walks
+// its words' flags that fall in the window.  Barriers at both ends.
+template <int NT>
+__device__ __forceinline__ void select_list(const uint8_t* __restrict__ f, int total, int lo, int win, int* map,
+                                            int* ws) {
+  const int t = tile_tid(), lane = t & 63, w = t >> 6;
+  const uint32_t* __restrict__ fw = reinterpret_cast<const uint32_t*>(f);
+  const int words = (total + 3) >> 2, per = (words + NT - 1) / NT;
+  const int x0 = min(words, t * per), x1 = min(words, x0 + per);
+  int c = 0;
+  for (int x = x0; x < x1; ++x) c += flag_sum(flag_word(fw, total, x));
+  int inc = c;   // inclusive prefix in the wave
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(inc, o);
+    if (lane >= o) inc += y;
+  }
+  if (lane == 63) ws[w] = inc;
+  __syncthreads();
+  int pos = inc - c;
+#pragma unroll
+  for (int q = 0; q < NT / 64; ++q) pos += q < w ? ws[q] : 0;
+  for (int x = x0; x < x1 && pos < lo + win; ++x) {
+    uint32_t v = flag_word(fw, total, x);
+    for (; v != 0u && pos < lo + win; v &= v - 1u, ++pos)
+      if (pos >= lo) map[pos - lo] = 4 * x + (__builtin_ctz(v) >> 3);
+  }
+  __syncthreads();
+}
+
+// A unit of a product whose prep found NaN / Inf rows or columns computes, if any, one tile of the
+// finite rows x finite columns (every other entry takes the safety fallback, which uses neither
+// digits nor L): the tcm x tcn tiles over the finite-row and finite-column lists (prep's flags) are
+// dealt to every s-th of the product's units in raster order, s = units / tiles, from a rotating
+// offset, so that they spread over the dispatch chunks and with them over the XCDs (the first
+// units of a product share one chunk); the other units end after the count.  The lists' windows go to the
+// tile-check LDS area after the ring, the operand pieces are gathered row by row, and the epilogue
+// stores each entry at its own row and column: the digits and L of the finite entries are those of
+// the whole product's tiles, since an entry's products do not depend on its tile.
+template <class C, bool kPacked>
+__device__ __forceinline__ void compacted_tile(uint8_t* lds, const i8_problem* __restrict__ probs,
+                                               const I8Epi* __restrict__ epis, const Unit& t, const YDesc* yd) {
+  static_assert(C::BM + C::BN <= kTileCheckBytes / 4, "list windows in the tile-check area");
+  static_assert(C::BM == 256 && C::BN == 256, "units of the large-tile raster");
+  const i8_problem& P = probs[t.pi];
+  int* const ws = reinterpret_cast<int*>(lds);   // the ring is idle until the prologue below
+  // the descriptor is constant in this kernel: scalar loads
+  const auto* const ydc = (const __attribute__((address_space(4))) YDesc*)yd;
+  const uint8_t* const fr = ydc->fr;
+  const uint8_t* const fc = ydc->fc;
+  const int2 cnt = count_lists<C::NT>(fr, P.m, fc, P.n, ws);
+  const int tcm = (cnt.x + C::BM - 1) / C::BM, tcn = (cnt.y + C::BN - 1) / C::BN, nt = tcm * tcn;
+  if (nt == 0) return;   // workgroup-uniform
+  const int units = ((P.m + C::BM - 1) / C::BM) * ((P.n + C::BN - 1) / C::BN);
+  // tile i at local unit off + i s, off = (pi kChunkL) mod s: the product's first tile rotates over
+  // its chunks from product to product
+  const int s = units / nt, off = (int)(((unsigned)t.pi * (unsigned)kChunkL) % (unsigned)s);
+  const int local = raster_local<kGroupML>(t.tm, t.tn, P.m, P.n, C::BM, C::BN) - off;
+  if (local < 0 || local % s != 0 || local / s >= nt) return;
+  const int i = local / s, cm = i % tcm, cn = i / tcm;
+  int* const rmap = reinterpret_cast<int*>(lds + C::SMEM);
+  int* const cmap = rmap + C::BM;
+  int* const ws2 = ws + 2 * (C::NT / 64);   // the counts' words may still be read
+  select_list<C::NT>(fr, P.m, cm * C::BM, C::BM, rmap, ws2);
+  select_list<C::NT>(fc, P.n, cn * C::BN, C::BN, cmap, ws2);
+  const int nr = cnt.x - cm * C::BM, nc = cnt.y - cn * C::BN;
+  TileSrc<C, kPacked>(P, cm, cn, rmap, cmap, nr, nc).prologue(lds);
+  run_tile<C, kPacked, true>(lds, probs, epis, t.pi, cm, cn, [] {}, [] { return Unit{-1, 0, 0, 0}; }, rmap, cmap,
+                             nr, nc);
+}
+
+// One hardware-dispatched tile.  With the product's reconstruct descriptor given (epi.yd, 256 x
+// 256 tiles on packed residues) and its non-finite flag set by prep, the unit computes a compacted
+// tile instead (compacted_tile).  Otherwise, with the product's shifts given (epi.nf) and the flag
+// set, a tile whose rows or whose columns are all non-finite is dropped: every entry of it takes
+// the safety fallback.  Only on tiles of at least PRE stages.  Each wave DMAs 64 of the tile's row shifts and 64 of its
 // column shifts (indices clamped to the product: a clamped copy is the last row / column, which is
 // in the tile) to LDS after the ring, ahead of the first PRE stages, which are issued in the general
 // form (VM DMA instructions per wave and stage, no branch between them).  With the flag set (a
@@ -778,7 +980,19 @@ __device__ __forceinline__ void one_tile(uint8_t* lds, const i8_problem* __restr
   const i8_problem& P = probs[t.pi];
   const TileSrc<C, kPacked> src(P, t.tm, t.tn);
   const I8Epi e = epi_of(epis, t.pi);
-  if (e.nf != nullptr && P.kp > (PRE - 1) * C::BK) {   // workgroup-uniform
+  // compacted tiles in the 256 x 256 kernel on packed residues only: a second copy of the tile's k
+  // loop takes the general kernel past the 128 VGPRs of its two workgroups per CU, and the
+  // row-major copy the large kernel past its budget (spills); the others keep the tile check below
+  constexpr bool kCompact = C::kSplit && kPacked;
+  if (kCompact && e.yd != nullptr) {   // workgroup-uniform: a product whose finite rows / columns prep lists
+    // the flag first (a scalar load): a compacted product's units that hold no tile then end
+    // without any operand load in flight
+    if (*(const __attribute__((address_space(4))) int*)e.nf) {
+      if constexpr (kCompact) compacted_tile<C, kPacked>(lds, probs, epis, t, e.yd);
+      return;
+    }
+    src.prologue(lds);
+  } else if (e.nf != nullptr && P.kp > (PRE - 1) * C::BK) {   // workgroup-uniform
     // written by prep, an earlier kernel of the call, and constant here: a scalar load
     const int nff = *(const __attribute__((address_space(4))) int*)e.nf;
     const int lane = src.lane, wave = src.wave;

@@ -69,6 +69,7 @@ int setup(int dev) {
   h->max_A_elems = h->max_B_elems = h->max_C_elems = kMaxElems;
   h->min_k = kKpAlign;
   h->packed_max_kp = kPackedMaxKp;
+  h->compact = 1;
   size_workspace(h, kMaxProblems, kMaxElems, kMaxElems, kMaxElems, kKpAlign);
   // the carve: A8 | B8 | C32 | row shifts | column shifts | descriptor blob, 256-byte aligned
   char* p = static_cast<char*>(base);

@@ -238,7 +238,7 @@ __device__ __forceinline__ void nf_header(GLOBAL int32_t* nfw, int ni, int nan, 
 template <bool kWide>
 __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ tab, int blk, int split,
                           int nsplit, PrepShared& sm, unsigned long long* cnt, int widx, bool packed, int32_t* nfo,
-                          int* nff, bool zero_nf) {
+                          int* nff, bool zero_nf, const YDesc* yds, int pi) {
   const int tid = threadIdx.x;
   // split 0, when the call asks for summaries: pass 1, which reads every value of the block's rows,
   // also collects each row's non-finite summary state (NaN seen, largest finite magnitude,
@@ -354,6 +354,9 @@ __device__ void prep_rows(const oz2_problem& pr, const CrtTables* __restrict__ t
     }
   }
   __syncthreads();
+  // the rows' finite flags (the descriptor is formed here, not kept live through the pass)
+  uint8_t* const frw = (split == 0 && yds) ? yds[pi].fr : nullptr;
+  if (frw && tid < kARows && row0 + tid < m) frw[row0 + tid] = sm.shift[tid] != OZ2_SHIFT_NONFINITE ? 1 : 0;
 
   // ---- pass 2: residues of this split's k-tiles; split 0 also walks every tile for the
   //      ordered ||dA||, ||A'|| chain sums (the residue values do not depend on the split)
@@ -440,7 +443,7 @@ constexpr int kBReg = 32;   // column values per lane held in registers (K <= 32
 template <bool kWide>
 __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ tab, int blk, int split,
                           int nsplit, PrepShared& sm, unsigned long long* cnt, bool packed, int32_t* nfo, int* nff,
-                          bool zero_nf) {
+                          bool zero_nf, const YDesc* yds, int pi) {
   const int lane = threadIdx.x & 31, w = threadIdx.x >> 5;
   const int j = blk * kBCols + w;
   const int n = pr.n, N = pr.num_moduli, K = pr.k, Kp = pr.kp;
@@ -575,6 +578,10 @@ __device__ void prep_cols(const oz2_problem& pr, const CrtTables* __restrict__ t
       atomicAdd(counter_slot(cnt), 1ull);
       if (nff) *nff = 1;
     }
+  }
+  if (split == 0 && yds && lane == 0) {   // the column's finite flag
+    uint8_t* const fcw = yds[pi].fc;
+    if (fcw) fcw[j] = sh != OZ2_SHIFT_NONFINITE ? 1 : 0;
   }
   const bool nf = sh == OZ2_SHIFT_NONFINITE;
 
@@ -715,9 +722,9 @@ __global__ void __launch_bounds__(kThreads, 4) prep_kernel(const oz2_problem* __
   const bool zero_nf = !fold_q;
   if (blk < a_blocks) {
     if (blk * kARows >= pr.m) return;
-    prep_rows<kWide>(pr, tab, blk, blockIdx.z, gridDim.z, sm, cnt, fold ? N : 0, packed, nfo, nff, zero_nf);
+    prep_rows<kWide>(pr, tab, blk, blockIdx.z, gridDim.z, sm, cnt, fold ? N : 0, packed, nfo, nff, zero_nf, yds, pi);
   } else {
-    prep_cols<kWide>(pr, tab, blk - a_blocks, blockIdx.z, gridDim.z, sm, cnt, packed, nfo, nff, zero_nf);
+    prep_cols<kWide>(pr, tab, blk - a_blocks, blockIdx.z, gridDim.z, sm, cnt, packed, nfo, nff, zero_nf, yds, pi);
   }
 }
 

@@ -446,6 +446,40 @@ def test_nonfinite_tiles_skipped(kernel, sched):
     assert tot[3] == 300 * 200 + 256 * 260 + 256 * 96 + 100 * 90
 
 
+def test_compacted_tiles():
+    """Products with NaN / Inf rows and columns in the large-tile kernel on packed residues compute
+    only their finite rows x finite columns, in tiles over prep's finite-row and finite-column lists
+    dealt to every s-th unit: the bits and counters equal the oracle's and those of a handle that
+    computes every tile (GGEMM_COMPACT=0).  Lists of 2 x 2 tiles over a 3 x 3 grid with m, n not
+    multiples of 4 (the lists' padding bytes), exactly 257 finite rows (a one-row second tile
+    row), 4 x 4 tiles filling a 5 x 5 grid, no finite row, a finite product, and kp = 4000 (a
+    half last k-block) with alpha != 1, beta != 0."""
+    shapes = [(601, 523, 300, 1.0, 0.0), (300, 700, 130, -1.5, 0.5), (1030, 1100, 200, 1.0, 0.0),
+              (512, 512, 64, 1.0, 0.0), (256, 256, 96, 1.0, 0.0), (700, 300, 4000, 2.0, 0.25)]
+    rates = [(0.55, 0.5), (43, 0.3), (0.1, 0.1), (1.0, 0.0), (0.0, 0.0), (0.5, 0.5)]
+    case = Case(shapes, 20261290, phi=2.0)
+    rng = np.random.default_rng(90)
+    bad = [np.nan, np.inf, -np.inf]
+
+    def spoiled(count, rate):
+        if isinstance(rate, float):
+            return [x for x in range(count) if rng.random() < rate]
+        return sorted(rng.choice(count, rate, replace=False).tolist())
+
+    for h, (rr, cr) in zip(case.hp, rates):
+        for i in spoiled(h.m, rr):
+            h.A[i + int(rng.integers(0, h.k)) * h.lda] = bad[i % 3]
+        for j in spoiled(h.n, cr):
+            h.B[int(rng.integers(0, h.k)) + j * h.ldb] = bad[j % 3]
+    case.alloc()
+    outs = []
+    for env in ({}, {"GGEMM_COMPACT": "0"}):
+        say(f"compacted tiles, large kernel, {env}")
+        outs.append(run_kernel(case, "large", **env))
+    for a, b in zip(*outs):
+        assert same_bits(a, b)
+
+
 def env_handle(case, min_k=None, **env):
     """A handle created with environment variables set (read at creation)."""
     saved = dict(os.environ)
