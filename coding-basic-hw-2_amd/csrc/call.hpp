@@ -28,6 +28,7 @@ struct GroupedCall {
   BlobLayout L{};
   i8_sched_info i8info{};
   int i8_kernel = kI8General;     // INT8 GEMM kernel the schedule was built for
+  int i8_hw = -1;                 // large-tile kernel: units dispatched one workgroup each (-1: all)
   bool blocked = false;           // digit and abs planes in the blocked layout
   bool packed = false;            // every problem's residue planes in the packed layout
   int packed_kp = 0;              // problems with Kp at most this (> 0) use the packed layout

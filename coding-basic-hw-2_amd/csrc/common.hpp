@@ -86,7 +86,7 @@ struct F64Problem {
 //   of the persistent kernel (zero when uploaded, reset by the kernel itself),
 //   prefix[entries + 1] at kSchedHdr (first tile of each entry), entry[entries] = (problem << 2) | cfg.
 constexpr int kXcds = 8;   // MI355X: accelerator complex dies, each with its own L2
-constexpr int kHdrXcd = 8, kHdrCtr = 32, kHdrDone = 40;
+constexpr int kHdrHw = 4, kHdrXcd = 8, kHdrCtr = 32, kHdrDone = 40;
 constexpr int kSchedHdr = 64;
 inline size_t sched_bytes(int entries) {
   return sizeof(int) * (size_t)(kSchedHdr + 2 * (size_t)entries + 1 + 8);
@@ -157,10 +157,15 @@ enum { kI8General = 0, kI8Large = 1, kI8Persistent = 2 };
 // large: kLargeNever, kLargeAuto (the large-tile kernel when every product is on automatic large
 // tiles and they fill the GPU) or kLargeForce (whenever every product's tile is automatic);
 // persistent: schedule for the persistent kernels (queues per XCD);
-// *kernel receives the choice, which i8_launch must be given.
+// *kernel receives the choice, which i8_launch must be given.  epis (host copies, or nullptr):
+// with the large-tile kernel dispatched one workgroup per tile, the products that may compact
+// (packed residues and a reconstruct descriptor) go last in the table, and *hw_units receives the
+// units before them, which i8_launch must be given: those run one workgroup each, the rest are
+// taken in chunks by as many workgroups as there are compute units (-1: every unit dispatched).
 enum { kLargeNever = 0, kLargeAuto = 1, kLargeForce = 2 };
 int i8_build_schedule(const i8_problem* h, int num, void* h_ws, size_t ws_bytes, i8_sched_info* info,
-                      int num_cus, int large = kLargeNever, int* kernel = nullptr, bool persistent = false);
+                      int num_cus, int large = kLargeNever, int* kernel = nullptr, bool persistent = false,
+                      const I8Epi* epis = nullptr, int* hw_units = nullptr);
 // The tile configuration i8_build_schedule gives an m x n product with tile_cfg < 0 (before the
 // group-level shrink).
 int i8_auto_tile_cfg(int m, int n);
@@ -172,7 +177,7 @@ void i8_reserve_host(size_t entries);
 bool i8_env_persistent();
 // d_epi: per-problem epilogues in device memory, or nullptr for int32 products everywhere.
 int i8_launch(const i8_problem* d_probs, const I8Epi* d_epi, const void* d_sched, const i8_sched_info* info,
-              hipStream_t s, int kernel = kI8General);
+              hipStream_t s, int kernel = kI8General, int hw_units = -1);
 
 // Where the reconstruct reads a problem's plane products in the production pipeline: CRT digits
 // y_l (one byte per entry, plane l at Y + l * y_stride) and the abs-plane product L (int32), both

@@ -440,7 +440,7 @@ int build_grouped(ggemm_handle_t h, const ggemm_problem_t* probs, int num, const
   if (c.nn && f64_build_schedule(hf, c.nn, hb + c.L.off_sf64, s_f64, &c.f64_tiles, nullptr, h->f64_tile))
     return GGEMM_ERR_INVALID;
   if (c.ne && i8_build_schedule(hi8, (int)c.n_i8, hb + c.L.off_si8, s_i8, &c.i8info, h->num_cus, large_mode(h, c),
-                                   &c.i8_kernel, h->i8_persistent != 0))
+                                   &c.i8_kernel, h->i8_persistent != 0, hepi, &c.i8_hw))
     return GGEMM_ERR_I8GEMM;
   c.h2d_bytes = c.ne ? c.L.off_si8 + c.i8info.bytes_used : c.L.off_si8;
   *out = c;
@@ -461,7 +461,7 @@ int enqueue_grouped(const GroupedCall& c, const char* db, hipStream_t s, int rep
     ++*launches;
     prof::mark(prof_set, 1, s);
     if (i8_launch(reinterpret_cast<const i8_problem*>(db + c.L.off_i8), reinterpret_cast<const I8Epi*>(db + c.L.off_epi),
-                  db + c.L.off_si8, &c.i8info, s, c.i8_kernel))
+                  db + c.L.off_si8, &c.i8info, s, c.i8_kernel, c.i8_hw))
       return GGEMM_ERR_I8GEMM;
     *launches += c.i8info.num_launches;
     prof::last_i8 = c.i8_kernel;

@@ -839,10 +839,10 @@ __device__ __forceinline__ void persistent(int* __restrict__ sched, const i8_pro
 // launcher).  Workgroup b takes tile chunk (b mod 8) + 8 (b / (8 CH)) of CH consecutive tiles of the
 // table, so one XCD works through contiguous runs (general kernel CH = 32: a 1024^2 product's 32
 // tiles share one L2 and each plane is read from HBM once; large-tile kernel CH = 16).
-constexpr int kChunk = 32, kChunkL = 16;
+constexpr int kChunk = 32, kChunkL = 16, kChunkT = 32;
+// (workgroup b of the first `total` ones)
 template <int CH>
-__device__ __forceinline__ int dispatched_unit(const int* __restrict__ sched) {
-  const int total = sched[0];
+__device__ __forceinline__ int dispatched_unit(int total) {
   const int b = blockIdx.x;
   const int span = kXcds * CH;
   const int full = total / span * span;
@@ -1029,7 +1029,7 @@ __global__ void __launch_bounds__(kThreads, 2) i8_grouped_kernel(const i8_proble
                                                                  const I8Epi* __restrict__ epis,
                                                                  int* __restrict__ sched) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
-  const Unit t = decode_unit<kGroupM, false>(sched, probs, dispatched_unit<kChunk>(sched));
+  const Unit t = decode_unit<kGroupM, false>(sched, probs, dispatched_unit<kChunk>(sched[0]));
   const bool pk = (epi_of(epis, t.pi).mode & kEpiPacked) != 0;
   switch (t.cfg) {
     case 0: pk ? one_tile<Cfg0, true>(lds, probs, epis, t) : one_tile<Cfg0, false>(lds, probs, epis, t); break;
@@ -1038,14 +1038,112 @@ __global__ void __launch_bounds__(kThreads, 2) i8_grouped_kernel(const i8_proble
   }
 }
 
-// every tile of the schedule is a 256 x 256 tile
+// Every tile of the schedule is a 256 x 256 tile.  Workgroups below hw = sched[kHdrHw] take one
+// unit each (the units [0, hw)); the tail workgroups, the rest of the grid, take the units [hw,
+// total) in chunks of kChunkL: chunk w for tail workgroup w, then the chunks after the tail's first
+// ones from a counter (the products that may compact go there, so that their units without a tile
+// cost a loop step, not a workgroup dispatch).  Each unit as one_tile; before the next one every
+// memory operation of the last one is complete (one_tile's first wait assumes no other is in
+// flight) and every wave is past it (the LDS ring).  The last tail workgroup to finish resets the
+// counter for the next launch (a replayed graph).
 __global__ void __launch_bounds__(kThreadsL, 1) i8_large_kernel(const i8_problem* __restrict__ probs,
                                                                 const I8Epi* __restrict__ epis,
                                                                 int* __restrict__ sched) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
-  const Unit t = decode_unit<kGroupML, true>(sched, probs, dispatched_unit<kChunkL>(sched));
-  if (epi_of(epis, t.pi).mode & kEpiPacked) one_tile<CfgL, true>(lds, probs, epis, t);
-  else one_tile<CfgL128, false>(lds, probs, epis, t);
+  __shared__ int s_unit, s_hw, s_total, s_q;   // tail: the next unit (< 0: none), the header's hw and
+                                               // total, queues left behind (thread 0's state)
+  const int hw0 = sched[kHdrHw];
+  if ((int)blockIdx.x < hw0) {   // workgroup-uniform
+    const Unit t = decode_unit<kGroupML, true>(sched, probs, dispatched_unit<kChunkL>(hw0));
+    if (epi_of(epis, t.pi).mode & kEpiPacked) one_tile<CfgL, true>(lds, probs, epis, t);
+    else one_tile<CfgL128, false>(lds, probs, epis, t);
+    return;
+  }
+  // The tail's queues: queue q holds the chunks q, q + 8, q + 16, ... of kChunkT consecutive units
+  // of [hw, total); the tail workgroups of XCD q (blockIdx = q mod 8: the dispatcher deals
+  // workgroups to the XCDs round-robin) start on its local indices 0 .. n_q - 1 and then fetch
+  // n_q + counter q, so an XCD works through contiguous runs of units (a product's operand panels
+  // shared in its L2); an exhausted queue sends the workgroup to the next one in turn.  Thread 0
+  // keeps the state in LDS, not across the tile in registers.
+  if (threadIdx.x == 0) {
+    s_hw = hw0;
+    s_total = sched[0];
+    s_q = 0;
+  }
+  const int own = (int)blockIdx.x & (kXcds - 1);
+  auto tail_wgs = [&](int q) {   // tail workgroups of XCD q
+    const int f = s_hw + (((q - s_hw) % kXcds) + kXcds) % kXcds;
+    return f < (int)gridDim.x ? ((int)gridDim.x - f + kXcds - 1) / kXcds : 0;
+  };
+  auto unit_of = [&](int q, int l) {   // local index l of queue q -> unit, or -1 past its end
+    const long long v = s_hw + ((long long)(l / kChunkT) * kXcds + q) * kChunkT + l % kChunkT;
+    return v < s_total ? (int)v : -1;
+  };
+  // thread 0: the unit of local index l of the current queue, else the next queues' fetches; -1
+  // when every queue is exhausted
+  auto resolve = [&](int l) {
+    for (;;) {
+      const int q = (own + s_q) & (kXcds - 1);
+      const int v = unit_of(q, l);
+      if (v >= 0) return v;
+      if (++s_q == kXcds) return -1;
+      const int q2 = (own + s_q) & (kXcds - 1);
+      l = tail_wgs(q2) + atomicAdd(sched + kHdrCtr + q2, 1);
+    }
+  };
+  auto fetch = [&]() {   // thread 0: the next local index of the current queue
+    const int q = (own + s_q) & (kXcds - 1);
+    return s_q < kXcds ? tail_wgs(q) + atomicAdd(sched + kHdrCtr + q, 1) : 0;
+  };
+  if (threadIdx.x == 0) {
+    const int b = (int)blockIdx.x;
+    s_unit = resolve((b - (s_hw + (((own - s_hw) % kXcds) + kXcds) % kXcds)) / kXcds);
+  }
+  __syncthreads();
+  auto compacts = [&](const Unit& t) {   // its product lists finite rows / columns and prep flagged it
+    const I8Epi e = epi_of(epis, t.pi);
+    return e.yd != nullptr && *(const __attribute__((address_space(4))) int*)e.nf != 0;
+  };
+  // every tail unit is a 256 x 256 tile on packed residues.  A unit of a flagged product runs as
+  // compacted_tile; the others as tiles whose next unit's stages go out before the epilogue when
+  // that unit does not compact (run_tile's handoff), so that the epilogue's stores drain under them.
+  int u = __builtin_amdgcn_readfirstlane(s_unit);
+  bool pre = false;   // u's stages are in flight
+  int pend = 0;       // thread 0: the local index fetched for the next unit
+  while (u >= 0) {
+    const Unit t = decode_unit<kGroupML, true>(sched, probs, u);
+    if (!pre && compacts(t)) {
+      compacted_tile<CfgL, true>(lds, probs, epis, t, epi_of(epis, t.pi).yd);
+      if (threadIdx.x == 0) s_unit = s_q < kXcds ? resolve(fetch()) : -1;
+      __syncthreads();
+      u = __builtin_amdgcn_readfirstlane(s_unit);
+      continue;
+    }
+    if (!pre) TileSrc<CfgL, true>(probs[t.pi], t.tm, t.tn).prologue(lds);
+    int nu = -1;
+    pre = run_tile<CfgL, true, false>(
+        lds, probs, epis, t.pi, t.tm, t.tn,
+        [&]() {
+          if (threadIdx.x == 0) pend = fetch();
+        },
+        [&]() -> Unit {
+          if (threadIdx.x == 0) s_unit = s_q < kXcds ? resolve(pend) : -1;
+          asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+          nu = __builtin_amdgcn_readfirstlane(s_unit);
+          if (nu < 0) return Unit{-1, 0, 0, 0};
+          Unit nx = decode_unit<kGroupML, true>(sched, probs, nu);
+          if (compacts(nx)) nx.cfg = -1;   // no stages: it runs as a compacted tile
+          return nx;
+        });
+    u = nu;
+  }
+  if (threadIdx.x == 0) {   // every fetch of this workgroup has returned
+    __threadfence();
+    if (atomicAdd(sched + kHdrDone, 1) == (int)gridDim.x - hw0 - 1) {
+      for (int x = 0; x < kXcds; ++x) atomicExch(sched + kHdrCtr + x, 0);
+      atomicExch(sched + kHdrDone, 0);
+    }
+  }
 }
 
 // ---------------------------------------------------------------- persistent kernels
@@ -1184,10 +1282,11 @@ bool i8_env_persistent() {
 }
 
 int i8_build_schedule(const i8_problem* h, int num, void* h_ws, size_t ws_bytes, i8_sched_info* info, int num_cus,
-                      int large, int* kernel, bool persistent) {
+                      int large, int* kernel, bool persistent, const I8Epi* epis, int* hw_units) {
   if (num < 0 || (num > 0 && !h) || !h_ws || !info) return 1;
   if (ws_bytes < sched_bytes(num)) return 2;
   if (kernel) *kernel = kI8General;
+  if (hw_units) *hw_units = -1;
   std::lock_guard<std::mutex> lk(g_mu);
   if (!ensure_capacity((size_t)num)) return 6;
   Ent* const ents = g_ents;
@@ -1219,6 +1318,7 @@ int i8_build_schedule(const i8_problem* h, int num, void* h_ws, size_t ws_bytes,
   }
   // large-tile kernel: every product on automatic large tiles, and enough 256 x 256 tiles to give
   // every compute unit one
+  bool large_chosen = false;
   if (large != kLargeNever && ne > 0) {
     bool all = true;
     long long t = 0;
@@ -1232,6 +1332,7 @@ int i8_build_schedule(const i8_problem* h, int num, void* h_ws, size_t ws_bytes,
         e->tiles = ((h[e->prob].m + 255) / 256) * ((h[e->prob].n + 255) / 256);
         e->cost = 256.0 * 256.0 * (double)(h[e->prob].kp + 128);
       }
+      large_chosen = true;
       if (kernel) *kernel = kI8Large;
     }
   }
@@ -1273,6 +1374,27 @@ int i8_build_schedule(const i8_problem* h, int num, void* h_ws, size_t ws_bytes,
     for (int x = 0; x < kXcds; ++x) pos[x] = first[x];
     for (size_t j = 0; j < ne; ++j) order[pos[xq[j]]++] = (int)j;
   }
+  // large-tile kernel, one workgroup per tile: the products that may compact (packed residues and
+  // a reconstruct descriptor) after the others, each part in LPT order
+  auto compacts = [&](const Ent& e) {
+    return epis && (epis[e.prob].mode & kEpiPacked) != 0 && epis[e.prob].yd != nullptr;
+  };
+  long long hw = -1;
+  if (large_chosen && !persistent && epis) {
+    size_t k = 0;
+    hw = 0;
+    for (size_t j = 0; j < ne; ++j)
+      if (!compacts(ents[j])) {
+        order[k++] = (int)j;
+        hw += ents[j].tiles;
+      }
+    if (k == ne) {
+      hw = -1;   // nothing compacts: every unit dispatched
+    } else {
+      for (size_t j = 0; j < ne; ++j)
+        if (compacts(ents[j])) order[k++] = (int)j;
+    }
+  }
   int* img = static_cast<int*>(h_ws);
   int* prefix = img + kSchedHdr;
   int* entry = prefix + ne + 1;
@@ -1291,6 +1413,8 @@ int i8_build_schedule(const i8_problem* h, int num, void* h_ws, size_t ws_bytes,
   prefix[ne] = (int)tot;
   img[0] = (int)tot;
   img[1] = (int)ne;
+  img[kHdrHw] = hw >= 0 ? (int)hw : (int)tot;
+  if (hw_units) *hw_units = hw >= 0 ? (int)hw : -1;
   img[3] = persistent ? chunk : 0;
   bool same = ne > 0;
   for (size_t j = 1; j < ne && same; ++j) same = ents[j].tiles == ents[0].tiles;
@@ -1344,7 +1468,7 @@ void i8_reserve_host(size_t entries) {
 }
 
 int i8_launch(const i8_problem* d_probs, const I8Epi* d_epi, const void* d_sched, const i8_sched_info* info,
-              hipStream_t s, int kernel) {
+              hipStream_t s, int kernel, int hw_units) {
   if (!info) return 1;
   if (info->num_launches == 0 || info->tiles_main == 0) return 0;
   if (!d_probs || !d_sched) return 1;
@@ -1368,8 +1492,16 @@ int i8_launch(const i8_problem* d_probs, const I8Epi* d_epi, const void* d_sched
     else
       hipLaunchKernelGGL(i8_grouped_persistent_kernel, dim3(grid), dim3(kThreads), kSmem, s, d_probs, d_epi, sched);
   } else if (large) {
-    hipLaunchKernelGGL(i8_large_kernel, dim3((unsigned)info->tiles_main), dim3(kThreadsL), kSmemL, s, d_probs, d_epi,
-                       sched);
+    // units [0, hw_units) one workgroup each, then the tail: a workgroup per compute unit, at most
+    // one per chunk of the remaining units
+    unsigned grid = (unsigned)info->tiles_main;
+    if (hw_units >= 0 && hw_units < info->tiles_main) {
+      const DevCtx* c = dev_ctx();
+      if (!c) return 6;
+      const int chunks = (info->tiles_main - hw_units + kChunkL - 1) / kChunkL;
+      grid = (unsigned)hw_units + (unsigned)std::max(1, std::min(c->num_cus, chunks));
+    }
+    hipLaunchKernelGGL(i8_large_kernel, dim3(grid), dim3(kThreadsL), kSmemL, s, d_probs, d_epi, sched);
   } else {
     hipLaunchKernelGGL(i8_grouped_kernel, dim3((unsigned)info->tiles_main), dim3(kThreads), kSmem, s, d_probs, d_epi,
                        sched);

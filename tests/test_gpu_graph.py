@@ -196,14 +196,18 @@ def test_persistent_plan_replays_match_oracle():
         h.close()
 
 
-def test_plan_replays_alternate_nonfinite_and_finite_data():
+@pytest.mark.parametrize("kernel", ["auto", "large"])
+def test_plan_replays_alternate_nonfinite_and_finite_data(kernel):
     """One plan replayed on a data set with NaN / Inf entries and on a finite one, alternately
     (ggemm_plan_update_pointers between the runs), repair ON.  Prep marks problems with non-finite
     rows / columns and the reconstruct marks problems with flagged entries in the plan's device
     descriptors; a replay on finite data after one on non-finite data sees those marks still set
     and must take the general paths, so every run is compared with the oracle bit for bit.  In X
     every A row of problem 0 and every B column of problem 2 holds a non-finite value, so the INT8
-    GEMM skips their tiles there; on Y, with the marks still set, it must compute them."""
+    GEMM skips their tiles there; on Y, with the marks still set, it must compute them.  kernel
+    large (GGEMM_I8_KERNEL at handle creation): the 256 x 256 kernel, whose packed products run in
+    its tail workgroups as compacted tiles over prep's finite-row / finite-column lists (on Y every
+    row and column, the marks still set) with the tail's queue counters reset by each replay."""
     shapes = [(200, 150, 300)] * 2 + [(64, 96, 1200), (130, 70, 40)]
     X = Case(shapes, 81, phi=2.0, alpha=1.5, beta=0.5)
     Y = Case(shapes, 82, phi=1.0, alpha=1.5, beta=0.5)
@@ -226,7 +230,15 @@ def test_plan_replays_alternate_nonfinite_and_finite_data():
     for name, case in (("X", X), ("Y", Y)):
         want[name] = [hp.emulate(O.REPAIR_ON, e.num_moduli) for hp, e in zip(case.hp, plan_o)]
     assert sum(int(c[3]) for _, c in want["X"]) > 0 and sum(int(c[3]) for _, c in want["Y"]) == 0
-    h = G.Handle(len(shapes), *[max(a, b) for a, b in zip(X.sizes(), Y.sizes())])
+    import os
+    saved = dict(os.environ)
+    if kernel == "large":
+        os.environ["GGEMM_I8_KERNEL"] = "large"
+    try:
+        h = G.Handle(len(shapes), *[max(a, b) for a, b in zip(X.sizes(), Y.sizes())])
+    finally:
+        os.environ.clear()
+        os.environ.update(saved)
     arr = G.problems_array(X.problems())
     err = C.c_int(0)
     plan = G.lib().ggemm_make_plan_ex(h.h, G.PATH_EMU_GROUPED, C.byref(cfg), arr, len(shapes), C.byref(err))
@@ -237,9 +249,11 @@ def test_plan_replays_alternate_nonfinite_and_finite_data():
             case = X if name == "X" else Y
             case.reset_C()
             assert G.lib().ggemm_plan_update_pointers(plan, ptr(case.dA), ptr(case.dB), ptr(case.dC)) == 0
-            say(f"plan replay {rep} on {name}")
+            say(f"plan replay {rep} on {name}, {kernel} kernel")
             assert G.lib().ggemm_execute_plan(plan, None) == 0
             torch.cuda.synchronize()
+            if kernel == "large":
+                assert G.lib().ggemm_profile_i8_kernel().decode() == "i8_large_kernel"
             for g, (Co, _) in enumerate(want[name]):
                 assert same_bits(case.C(g), Co), f"replay {rep} ({name}): problem {g} differs"
     finally:
