@@ -1493,13 +1493,12 @@ int i8_launch(const i8_problem* d_probs, const I8Epi* d_epi, const void* d_sched
       hipLaunchKernelGGL(i8_grouped_persistent_kernel, dim3(grid), dim3(kThreads), kSmem, s, d_probs, d_epi, sched);
   } else if (large) {
     // units [0, hw_units) one workgroup each, then the tail: a workgroup per compute unit, at most
-    // one per chunk of the remaining units
+    // one per remaining unit
     unsigned grid = (unsigned)info->tiles_main;
     if (hw_units >= 0 && hw_units < info->tiles_main) {
       const DevCtx* c = dev_ctx();
       if (!c) return 6;
-      const int chunks = (info->tiles_main - hw_units + kChunkL - 1) / kChunkL;
-      grid = (unsigned)hw_units + (unsigned)std::max(1, std::min(c->num_cus, chunks));
+      grid = (unsigned)hw_units + (unsigned)std::max(1, std::min(c->num_cus, info->tiles_main - hw_units));
     }
     hipLaunchKernelGGL(i8_large_kernel, dim3(grid), dim3(kThreadsL), kSmemL, s, d_probs, d_epi, sched);
   } else {
