@@ -1038,18 +1038,23 @@ __global__ void __launch_bounds__(kThreads, 2) i8_grouped_kernel(const i8_proble
   }
 }
 
-// Every tile of the schedule is a 256 x 256 tile.  Workgroups below hw = sched[kHdrHw] take one
-// unit each (the units [0, hw)); the tail workgroups, the rest of the grid, take the units [hw,
-// total) in chunks of kChunkL: chunk w for tail workgroup w, then the chunks after the tail's first
-// ones from a counter (the products that may compact go there, so that their units without a tile
-// cost a loop step, not a workgroup dispatch).  Each unit as one_tile; before the next one every
-// memory operation of the last one is complete (one_tile's first wait assumes no other is in
-// flight) and every wave is past it (the LDS ring).  The last tail workgroup to finish resets the
-// counter for the next launch (a replayed graph).
+// Every tile of the schedule is a 256 x 256 tile.  kTail false: one workgroup per unit.  kTail
+// true (launched when the schedule puts the products that may compact last, sched[kHdrHw] = hw
+// units before them): workgroups below hw take one unit each, and the tail workgroups, the rest of
+// the grid, take the units [hw, total) from work queues (below), so that a compacting product's
+// units without a tile cost a loop step, not a workgroup dispatch.  Two instantiations, so that the
+// one-workgroup-per-unit kernel keeps its registers and code without the tail loop.
+template <bool kTail>
 __global__ void __launch_bounds__(kThreadsL, 1) i8_large_kernel(const i8_problem* __restrict__ probs,
                                                                 const I8Epi* __restrict__ epis,
                                                                 int* __restrict__ sched) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+  if constexpr (!kTail) {
+    const Unit t = decode_unit<kGroupML, true>(sched, probs, dispatched_unit<kChunkL>(sched[0]));
+    if (epi_of(epis, t.pi).mode & kEpiPacked) one_tile<CfgL, true>(lds, probs, epis, t);
+    else one_tile<CfgL128, false>(lds, probs, epis, t);
+    return;
+  }
   __shared__ int s_unit, s_hw, s_total, s_q;   // tail: the next unit (< 0: none), the header's hw and
                                                // total, queues left behind (thread 0's state)
   const int hw0 = sched[kHdrHw];
@@ -1445,8 +1450,10 @@ bool lds_attrs_set() {
   if (!done[dev]) {
     if (hipFuncSetAttribute((const void*)i8_grouped_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kSmem) !=
             hipSuccess ||
-        hipFuncSetAttribute((const void*)i8_large_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kSmemL) !=
-            hipSuccess ||
+        hipFuncSetAttribute((const void*)i8_large_kernel<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            kSmemL) != hipSuccess ||
+        hipFuncSetAttribute((const void*)i8_large_kernel<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            kSmemL) != hipSuccess ||
         hipFuncSetAttribute((const void*)i8_grouped_persistent_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                             kSmem) != hipSuccess ||
         hipFuncSetAttribute((const void*)i8_large_persistent_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -1492,15 +1499,20 @@ int i8_launch(const i8_problem* d_probs, const I8Epi* d_epi, const void* d_sched
     else
       hipLaunchKernelGGL(i8_grouped_persistent_kernel, dim3(grid), dim3(kThreads), kSmem, s, d_probs, d_epi, sched);
   } else if (large) {
-    // units [0, hw_units) one workgroup each, then the tail: a workgroup per compute unit, at most
-    // one per remaining unit
+    // units [0, hw_units) one workgroup each, then the tail: a workgroup per compute unit over the
+    // rest (when there are fewer of them, one workgroup per unit throughout)
     unsigned grid = (unsigned)info->tiles_main;
+    bool tail = false;
     if (hw_units >= 0 && hw_units < info->tiles_main) {
       const DevCtx* c = dev_ctx();
       if (!c) return 6;
-      grid = (unsigned)hw_units + (unsigned)std::max(1, std::min(c->num_cus, info->tiles_main - hw_units));
+      tail = info->tiles_main - hw_units > c->num_cus;
+      if (tail) grid = (unsigned)(hw_units + c->num_cus);
     }
-    hipLaunchKernelGGL(i8_large_kernel, dim3(grid), dim3(kThreadsL), kSmemL, s, d_probs, d_epi, sched);
+    if (tail)
+      hipLaunchKernelGGL(i8_large_kernel<true>, dim3(grid), dim3(kThreadsL), kSmemL, s, d_probs, d_epi, sched);
+    else
+      hipLaunchKernelGGL(i8_large_kernel<false>, dim3(grid), dim3(kThreadsL), kSmemL, s, d_probs, d_epi, sched);
   } else {
     hipLaunchKernelGGL(i8_grouped_kernel, dim3((unsigned)info->tiles_main), dim3(kThreads), kSmem, s, d_probs, d_epi,
                        sched);

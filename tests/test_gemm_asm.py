@@ -42,6 +42,7 @@ def test_int8_gemm_kernels_wait_before_use(tmp_path):
     r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
     if r.returncode != 0:
         pytest.fail(r.stderr[-2000:])
-    for kernel in ("i8_grouped_kernel", "i8_large_kernel", "i8_grouped_persistent_kernel", "i8_large_persistent_kernel"):
+    for kernel in ("i8_grouped_kernel", "i8_large_kernelILb0", "i8_large_kernelILb1", "i8_grouped_persistent_kernel",
+                   "i8_large_persistent_kernel"):
         found = L.check(out, kernel)
         assert not found, f"{kernel}: {found[:4]}"
