@@ -306,9 +306,10 @@ def main():
     i8_kernel = G.lib().ggemm_profile_i8_kernel().decode()
     st_ms = [stage[q] / max(ncalls.value, 1) for q in range(4)]
     i8_ms = st_ms[1]
-    # with non-finite data the dispatched INT8 kernels skip tiles that have no finite row or no
-    # finite column (their entries all take the safety fallback): the roofline counts the
-    # operations of the computed tiles (large-tile kernel: 256 x 256 tiles, checked when kp > 192)
+    # with non-finite data the large-tile kernel computes, of a product on packed residues (kp <=
+    # 4096), only its finite rows x finite columns, and of the others the 256 x 256 tiles with a
+    # finite row and a finite column (checked when kp > 192); every other entry takes the safety
+    # fallback: the roofline counts the operations of that finite sub-grid / of those tiles
     computed_ops, skipped_share = int8_ops, 0.0
     fin = {g: (shapes[g][0], shapes[g][1]) for g in emu}   # finite rows of A, finite columns of B
     if bad > 0.0 and emu:
@@ -321,6 +322,9 @@ def main():
             fin[g] = (int(rf.sum().item()), int(cf.sum().item()))
             tr = torch.nn.functional.pad(rf, (0, (-m) % 256)).view(-1, 256).any(dim=1)
             tc = torch.nn.functional.pad(cf, (0, (-n) % 256)).view(-1, 256).any(dim=1)
+            if kp <= 4096:   # packed residues: the finite sub-grid
+                computed_ops += (plan_e[g].num_moduli + 1) * 2.0 * fin[g][0] * fin[g][1] * kp
+                continue
             live = int((tr[:, None] & tc[None, :]).sum().item()) if kp > 192 else tr.numel() * tc.numel()
             computed_ops += (plan_e[g].num_moduli + 1) * 2.0 * m * n * kp * live / (tr.numel() * tc.numel())
         skipped_share = 1.0 - computed_ops / int8_ops
