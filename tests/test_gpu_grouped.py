@@ -480,6 +480,33 @@ def test_compacted_tiles():
         assert same_bits(a, b)
 
 
+def test_tail_workgroups_mixed_units():
+    """The 256 x 256 kernel's tail workgroups over more units than compute units (four finite
+    768 x 768 x 512 products, 9 tiles x 16 planes each, so every workgroup runs a chain of units,
+    the next unit's stages issued before the epilogue), with a product with NaN / Inf rows and
+    columns among them (compacted tiles and units without one between finite tiles) and a short
+    finite product: bits and counters equal the oracle's and those of one workgroup per tile
+    (GGEMM_COMPACT=0)."""
+    shapes = [(768, 768, 512, 1.0, 0.0)] * 4 + [(600, 520, 300, -1.0, 0.5), (512, 512, 64, 1.0, 0.0)]
+    case = Case(shapes, 20261291, phi=1.0)
+    rng = np.random.default_rng(91)
+    bad = [np.nan, np.inf, -np.inf]
+    h = case.hp[4]
+    for i in range(h.m):
+        if rng.random() < 0.6:
+            h.A[i + int(rng.integers(0, h.k)) * h.lda] = bad[i % 3]
+    for j in range(h.n):
+        if rng.random() < 0.5:
+            h.B[int(rng.integers(0, h.k)) + j * h.ldb] = bad[j % 3]
+    case.alloc()
+    outs = []
+    for env in ({}, {"GGEMM_COMPACT": "0"}):
+        say(f"tail workgroups, mixed units, {env}")
+        outs.append(run_kernel(case, "large", **env))
+    for a, b in zip(*outs):
+        assert same_bits(a, b)
+
+
 def env_handle(case, min_k=None, **env):
     """A handle created with environment variables set (read at creation)."""
     saved = dict(os.environ)
