@@ -210,3 +210,105 @@ def test_chunked_queues_cover_every_tile(chunk):
     total = int(img[0])
     runs, _ = run_protocol(img, min(total, 512), random.Random(3))
     assert sorted(u for r in runs for u in r) == list(range(total))
+
+
+def run_tail(hw, total, grid, rng, chunk=32):
+    """Model of the 256 x 256 kernel's tail workgroups (i8_large_kernel<true>, blockIdx >= hw): the
+    queue q = chunks q, q + 8, ... of `chunk` units of [hw, total); a tail workgroup on XCD b mod 8
+    starts at its rank among that XCD's tail workgroups, then fetches from the queue's counter and
+    moves on to the next queues in turn.  The atomics are interleaved at random; returns the units
+    each workgroup ran and the counters left."""
+    ctr = [0] * XCDS
+
+    def tail_wgs(q):
+        f = hw + ((q - hw) % XCDS + XCDS) % XCDS
+        return (grid - f + XCDS - 1) // XCDS if f < grid else 0
+
+    def unit_of(q, l):
+        v = hw + ((l // chunk) * XCDS + q) * chunk + l % chunk
+        return v if v < total else -1
+
+    def workgroup(b):
+        own, sq = b % XCDS, 0
+        runs = []
+
+        def resolve(l):
+            nonlocal sq
+            while True:
+                v = unit_of((own + sq) % XCDS, l)
+                if v >= 0:
+                    return v
+                sq += 1
+                if sq == XCDS:
+                    return -1
+                q2 = (own + sq) % XCDS
+                l = tail_wgs(q2) + ctr[q2]
+                ctr[q2] += 1
+
+        first = hw + ((own - hw) % XCDS + XCDS) % XCDS
+        u = resolve((b - first) // XCDS)
+        while u >= 0:
+            runs.append(u)
+            yield None                      # a tile's work: other workgroups' atomics may interleave
+            if sq == XCDS:
+                break
+            q = (own + sq) % XCDS
+            l = tail_wgs(q) + ctr[q]
+            ctr[q] += 1
+            u = resolve(l)
+        yield runs
+
+    gens = {b: workgroup(b) for b in range(hw, grid)}
+    done = {}
+    while gens:
+        b = rng.choice(sorted(gens))
+        r = next(gens[b])
+        if r is not None:
+            done[b] = r
+            del gens[b]
+    return done, ctr
+
+
+@pytest.mark.parametrize("hw,total,grid", [(0, 40, 40), (0, 700, 256), (4096, 34816, 4096 + 256), (5, 1000, 5 + 256),
+                                           (0, 300, 7), (3, 3 + 65, 3 + 64), (100, 100 + 513, 100 + 256)])
+def test_tail_workgroups_run_every_unit_once(hw, total, grid):
+    """Every unit of the tail runs exactly once and every tail workgroup stops, under random
+    interleavings of the queue counters' atomics, with tails smaller and larger than the grid,
+    XCDs without tail workgroups (whose queues are stolen) and a first tail workgroup off XCD 0."""
+    for seed in range(3):
+        done, _ = run_tail(hw, total, grid, random.Random(seed))
+        units = sorted(u for r in done.values() for u in r)
+        assert units == list(range(hw, total))
+        assert sorted(done) == list(range(hw, grid))
+
+
+@pytest.mark.parametrize("m,n", [(2048, 2048), (300, 700), (1030, 1100), (256, 256), (2500, 300)])
+def test_compacted_tiles_dealt_once(m, n):
+    """The compacted tiles of a 256 x 256-tile product: for every list size, tile i goes to the unit at
+    raster index off + i s (s = units / tiles, off = 16 pi mod s), and the inverse of the raster
+    (the unit's local index from its tile position) finds each exactly once."""
+    bm = bn = 256
+    tiles_m, tiles_n = -(-m // bm), -(-n // bn)
+    units = tiles_m * tiles_n
+    pos = {raster(local, m, n, bm, bn, 4): local for local in range(units)}
+
+    def raster_local(tm, tn):   # the kernel's inverse raster (groups of 4 tile-rows)
+        g = tm // 4
+        first = g * 4
+        gsz = min(4, tiles_m - first)
+        return g * 4 * tiles_n + tn * gsz + (tm - first)
+
+    assert all(raster_local(*t) == local for t, local in pos.items())
+    for nrt in range(1, m + 1, max(1, m // 7)):
+        for nct in range(1, n + 1, max(1, n // 5)):
+            tcm, tcn = -(-nrt // bm), -(-nct // bn)
+            nt = tcm * tcn
+            for pi in (0, 1, 5, 37):
+                s = units // nt
+                off = (pi * 16) % s
+                got = []
+                for (tm, tn), _ in pos.items():
+                    local = raster_local(tm, tn) - off
+                    if local >= 0 and local % s == 0 and local // s < nt:
+                        got.append(local // s)
+                assert sorted(got) == list(range(nt))
