@@ -559,8 +559,9 @@ def test_dense_and_sparse_dot_forms(k, chains, form):
         assert tot[3] > 0
 
 
+@pytest.mark.parametrize("kernel", ["auto", "large"])
 @pytest.mark.parametrize("k", [3, 150, 1030])
-def test_repair_subgrid_dot_pass(k):
+def test_repair_subgrid_dot_pass(k, kernel):
     """Repairs concentrated in a sparse finite sub-grid (the hard config's pattern at reduced size):
     most rows of A and columns of B hold a NaN / Inf and phi = 4 leaves most finite-row x
     finite-column entries uncertified, so the dot pass decides the safety entries from the
@@ -572,7 +573,8 @@ def test_repair_subgrid_dot_pass(k):
     a single tile row over 520 and 4200 columns (5 regions), repair rows in half the rows of one tile
     row (m = 64, 1200 columns), and exactly 9 finite rows and 28 finite columns in every tile
     (m = 128, n = 1100: 18 rows x 448 columns of crossings in the first region, 2 x 28 blocks in two
-    passes); k below a k-chunk, k % 4 != 0, alpha != 1, beta != 0."""
+    passes); k below a k-chunk, k % 4 != 0, alpha != 1, beta != 0.  kernel large: the 256 x 256
+    INT8 kernel (GGEMM_I8_KERNEL), whose compacted tiles give the finite sub-grid's digits."""
     shapes = [(300, 280, k, -1.5, 0.5), (130, 300, k, 1.0, 0.0), (64, 520, k, 2.0, 1.0), (70, 4200, 40, 1.0, 0.0),
               (64, 1200, 60, 1.0, 0.25), (128, 1100, k, 0.5, 0.0)]
     # rows, columns with NaN / Inf: a rate, or exactly all but (9, 28) per 64-row / 64-column tile
@@ -600,8 +602,10 @@ def test_repair_subgrid_dot_pass(k):
         cfg = G.Config(0, 1e-15, 1, mode)
         outs = []
         for form in ("auto", "tile"):
-            say(f"repair sub-grid k={k} mode={mode} form={form}")
+            say(f"repair sub-grid k={k} mode={mode} form={form} kernel={kernel}")
             env = {} if form == "auto" else {"GGEMM_DOT_FORM": "tile"}
+            if kernel == "large":
+                env["GGEMM_I8_KERNEL"] = "large"
             with env_handle(case, min_k=1, **env) as hd:
                 rc, st = run(case, G.PATH_EMU_GROUPED, cfg, handle=hd)
             assert rc == 0
