@@ -80,10 +80,11 @@ struct F64Problem {
 
 // Schedule image shared by the tile-based kernels (INT8 GEMM, FP64 GEMM):
 //   int[0] total tiles, int[1] entries, int[2] tiles per entry when all entries have the same
-//   count (INT8 GEMM; 0 otherwise), int[3..7] reserved,
-//   INT8 GEMM only: int[kHdrXcd + x], x = 0..8, first tile of XCD x's queue (x = 8: the total);
-//   int[kHdrCtr + x], x < 8, the queue counters and int[kHdrDone] the finished-workgroup count
-//   of the persistent kernel (zero when uploaded, reset by the kernel itself),
+//   count (INT8 GEMM; 0 otherwise), int[3] the persistent queues' chunk, int[kHdrHw] the units the
+//   256 x 256 kernel dispatches one workgroup each (the rest go to its tail workgroups), int[5..7]
+//   reserved, INT8 GEMM only: int[kHdrXcd + x], x = 0..8, first tile of XCD x's queue (x = 8: the
+//   total); int[kHdrCtr + x], x < 8, the queue counters and int[kHdrDone] the finished-workgroup
+//   count of the persistent kernel and of the tail (zero when uploaded, reset by the kernel itself),
 //   prefix[entries + 1] at kSchedHdr (first tile of each entry), entry[entries] = (problem << 2) | cfg.
 constexpr int kXcds = 8;   // MI355X: accelerator complex dies, each with its own L2
 constexpr int kHdrHw = 4, kHdrXcd = 8, kHdrCtr = 32, kHdrDone = 40;
@@ -137,8 +138,9 @@ struct I8Epi {
   const int32_t* cs;
   const int* nf;
   // the product's reconstruct descriptor (blocked grouped calls, nullptr otherwise): with its
-  // non-finite flag set, the dispatched INT8 kernels compute only the finite rows x finite columns
-  // (its finite-row / finite-column lists, below), each tile over consecutive entries of the lists
+  // non-finite flag set, the 256 x 256 kernel on packed residues computes only the finite rows x
+  // finite columns (the descriptor's finite-row / finite-column lists), each tile over consecutive
+  // entries of the lists
   const YDesc* yd;
 };
 I8Epi i8_epi_residue(uint32_t p, int kp);

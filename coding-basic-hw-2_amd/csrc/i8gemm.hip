@@ -699,7 +699,9 @@ __device__ __forceinline__ bool run_tile(uint8_t* lds, const i8_problem* __restr
 // Schedule image (ints; built by i8_build_schedule):
 //   [0] units (tiles) in all, [1] entries, [2] tiles per entry when all entries have the same count
 //   (else 0), [3] chunk c (> 0: queue x is chunks x, x + 8, ... of c consecutive units instead of a
-//   range); [kHdrXcd + x], x = 0..8: first unit of XCD x's queue (x = 8: the total);
+//   range), [kHdrHw] the units the 256 x 256 kernel dispatches one workgroup each (its tail takes
+//   the rest, through the counters below); [kHdrXcd + x], x = 0..8: first unit of XCD x's queue
+//   (x = 8: the total);
 //   [kHdrCtr + x], x < 8: XCD x's queue counter, [kHdrDone]: workgroups finished -- zero in the
 //   uploaded image and reset by the last workgroup of every launch, so a captured graph replays
 //   without clearing them; prefix[entries + 1] at kSchedHdr (first unit of each entry),
