@@ -837,8 +837,9 @@ __device__ __forceinline__ void sparse_dots(const oz2_problem& pr, int r0, int c
   }
 }
 
-// (launch bounds: six waves per SIMD, which the chains' latency needs; seven spill)
-__global__ void __launch_bounds__(kThreads, 6) dots_kernel(const oz2_problem* __restrict__ probs,
+// (launch bounds: seven waves per SIMD, which the summaries' partner loads and the chains' latency
+// need, at a few spilled registers; six: 3-6 % slower on the hard config)
+__global__ void __launch_bounds__(kThreads, 7) dots_kernel(const oz2_problem* __restrict__ probs,
                                                         const YDesc* __restrict__ yds, int gne, int gper, int form) {
   __shared__ __attribute__((aligned(16))) double buf[kUnion];
   __shared__ uint64_t fl[64];       // flag words of the tile's 16 blocks (4 per block, column-major blocks)
