@@ -36,6 +36,12 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef double v2d __attribute__((ext_vector_type(2)));
+// the same vectors at element alignment: one 16-byte access wherever its 4 / 2 elements lie (gfx950
+// global memory takes dword-aligned vector accesses), for rows of C and of the shift arrays whose
+// stride m is not a multiple of 4 -- element-wise accesses there cost the reconstruct of a ragged
+// group a fifth of its time
+typedef int v4i_e __attribute__((ext_vector_type(4), aligned(4)));
+typedef double v2d_e __attribute__((ext_vector_type(2), aligned(8)));
 
 constexpr int kThreads = 256;
 constexpr int kTileM = 128, kTileN = 8;   // rows x columns per workgroup (32 row quads x 8 columns)
@@ -318,7 +324,8 @@ __global__ void __launch_bounds__(kThreads) recon_kernel(const oz2_problem* __re
   const bool active = N >= 1 && N <= kMaxModuli && m > 0 && n > 0 && i0 < m && j < n;
   const double alpha = pr.alpha, beta = pr.beta;
   const int ne = active ? min(4, m - i0) : 0;
-  const bool full = ne == 4 && (m & 3) == 0;
+  const bool four = ne == 4;                 // the thread's 4 rows exist
+  const bool full = four && (m & 3) == 0;   // ... and column-major digits are 4-byte aligned
   GLOBAL double* const cp = gpw(pr.C) + (active ? i0 + (size_t)j * pr.ldc : 0);
   unsigned dmask = 0;   // entries that take the FP64 dot product
   if (active) {
@@ -326,9 +333,9 @@ __global__ void __launch_bounds__(kThreads) recon_kernel(const oz2_problem* __re
     double out[4];
     // ---- loads
     if (beta != 0.0) {
-      if (full && ((reinterpret_cast<uintptr_t>(cp) & 15) == 0)) {
-        const v2d a = *reinterpret_cast<const GLOBAL v2d*>(cp);
-        const v2d b = *reinterpret_cast<const GLOBAL v2d*>(cp + 2);
+      if (four) {
+        const v2d_e a = *reinterpret_cast<const GLOBAL v2d_e*>(cp);
+        const v2d_e b = *reinterpret_cast<const GLOBAL v2d_e*>(cp + 2);
         c0[0] = a.x; c0[1] = a.y; c0[2] = b.x; c0[3] = b.y;
       } else {
         for (int e = 0; e < ne; ++e) c0[e] = cp[e];
@@ -341,11 +348,11 @@ __global__ void __launch_bounds__(kThreads) recon_kernel(const oz2_problem* __re
     if (alpha != 0.0) {
       const GLOBAL int32_t* rs = gp(pr.row_shift);
       const GLOBAL int32_t* cs = gp(pr.col_shift);
-      if (full) {
-        const v4i a = *reinterpret_cast<const GLOBAL v4i*>(rs + i0);
-        const v4i b = *reinterpret_cast<const GLOBAL v4i*>(rs + m + i0);
-        const v4i c = *reinterpret_cast<const GLOBAL v4i*>(rs + 2 * m + i0);
-        const v4i d = *reinterpret_cast<const GLOBAL v4i*>(rs + 3 * m + i0);
+      if (four) {
+        const v4i_e a = *reinterpret_cast<const GLOBAL v4i_e*>(rs + i0);
+        const v4i_e b = *reinterpret_cast<const GLOBAL v4i_e*>(rs + m + i0);
+        const v4i_e c = *reinterpret_cast<const GLOBAL v4i_e*>(rs + 2 * m + i0);
+        const v4i_e d = *reinterpret_cast<const GLOBAL v4i_e*>(rs + 3 * m + i0);
         rsh[0] = a.x; rsh[1] = a.y; rsh[2] = a.z; rsh[3] = a.w;
         sig[0] = b.x; sig[1] = b.y; sig[2] = b.z; sig[3] = b.w;
         dab[0] = c.x; dab[1] = c.y; dab[2] = c.z; dab[3] = c.w;
@@ -451,9 +458,9 @@ __global__ void __launch_bounds__(kThreads) recon_kernel(const oz2_problem* __re
         dmask |= dot ? 1u << e : 0u;
       }
     // certified entries now; entries taking the dot product keep C0 in C until then
-    if (dmask == 0u && full && ((reinterpret_cast<uintptr_t>(cp) & 15) == 0)) {
-      *reinterpret_cast<GLOBAL v2d*>(cp) = v2d{out[0], out[1]};
-      *reinterpret_cast<GLOBAL v2d*>(cp + 2) = v2d{out[2], out[3]};
+    if (dmask == 0u && four) {
+      *reinterpret_cast<GLOBAL v2d_e*>(cp) = v2d_e{out[0], out[1]};
+      *reinterpret_cast<GLOBAL v2d_e*>(cp + 2) = v2d_e{out[2], out[3]};
     } else {
       for (int e = 0; e < ne; ++e)
         if (!((dmask >> e) & 1u)) cp[e] = out[e];
