@@ -840,3 +840,23 @@ def test_bitwise_reproducible(path):
             assert rc == 0
             outs.append(np.concatenate([case.C(g) for g in range(len(case.hp))]))
         assert same_bits(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("pad", [1, 3])
+def test_padded_leading_dimensions(pad):
+    """Leading dimensions past m / k (lda = ldc = m + pad, ldb = k + pad): columns of C then start at
+    any 8-byte offset, so the reconstruct's 128-bit accesses of C (and of the shift arrays, whatever
+    m mod 4) read and write unaligned rows; beta != 0, a NaN row and an Inf column, repair ON;
+    bitwise against the oracle with equal counters."""
+    shapes = [(33, 17, 40), (64, 40, 100), (70, 66, 129), (130, 33, 64), (257, 48, 300)]
+    case = Case(shapes, 20261240 + pad, phi=1.0, beta=0.5, pad=pad)
+    h = case.hp[1]
+    h.A[5 + 7 * h.lda] = np.nan
+    h = case.hp[3]
+    h.B[10 + 20 * h.ldb] = np.inf
+    case.alloc()
+    cfg = G.Config(0, 1e-15, 0, G.REPAIR_ON)
+    say(f"padded leading dimensions, pad {pad}")
+    rc, st = run(case, G.PATH_EMU_GROUPED, cfg)
+    assert rc == 0
+    check_case(case, G.PATH_EMU_GROUPED, cfg, st, O.REPAIR_ON)
