@@ -111,15 +111,16 @@ def fill(torch, out, phi, seed, salt, lo_hi=None, nonfinite=0.0):
 
 
 def measured_traffic(workload, kernel):
-    """HBM bytes per launch of the INT8 GEMM kernel from the committed rocprofv3 counter summary
-    (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by its plain-copy calibration), or None
-    when no summary exists for this workload and kernel."""
+    """HBM bytes per launch of the roofline's kernel (the INT8 GEMM or prep) from the committed
+    rocprofv3 counter summary (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by its plain-copy
+    calibration), or None when no summary exists for this workload and kernel (template arguments
+    of the profiler's kernel name aside)."""
     f = REPO / "profiles" / "hbm_traffic.json"
     try:
         rec = json.loads(f.read_text()).get(workload)
     except (OSError, ValueError):
         return None
-    if not rec or rec.get("kernel") != kernel:
+    if not rec or str(rec.get("kernel", "")).split("<")[0] != kernel:
         return None
     return rec.get("traffic_bytes")
 
@@ -394,8 +395,8 @@ def main():
     if st_ms[0] > st_ms[1] and st_ms[0] > 0:
         prep_gbs = prep_bytes / (st_ms[0] * 1e-3) / 1e9
         roof = {"bound": "hbm", "kernel": "prep_kernel", "achieved": round(prep_gbs, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(prep_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                "int8_gemm": roof}
+                "unit": "GB/s", "frac": round(prep_gbs / HBM_PEAK_GBS, 4),
+                "traffic": measured_traffic(args.workload, "prep_kernel"), "int8_gemm": roof}
     out = {
         "metric": "effective FP64 TFLOP/s (2*sum mnk/t), % INT8 MFMA peak, max certified rel err",
         "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,

@@ -199,12 +199,15 @@ def traffic(args):
 
 
 def write_traffic_json(args, kt):
-    """Record the INT8 GEMM's HBM bytes per launch under args.traffic_key in args.traffic_json (the
-    figure bench.py reports as roofline.traffic); other keys of an existing file are kept."""
+    """Record the HBM bytes per launch of the busiest kernel of stage args.traffic_stage (the INT8
+    GEMM by default, prep for a call whose dominant kernel is prep) under args.traffic_key in
+    args.traffic_json (the figure bench.py reports as roofline.traffic); other keys of an existing
+    file are kept."""
     det = traffic_detail(args)
-    gemm = [k for k in det if stage_of(k) == "i8_gemm"]
+    stage = getattr(args, "traffic_stage", None) or "i8_gemm"
+    gemm = [k for k in det if stage_of(k) == stage]
     if not gemm:
-        raise SystemExit("--traffic-json: no INT8 GEMM kernel with FETCH_SIZE and WRITE_SIZE counters")
+        raise SystemExit(f"--traffic-json: no {stage} kernel with FETCH_SIZE and WRITE_SIZE counters")
     k = max(gemm, key=lambda g: kt[g][1] * kt[g][2] if g in kt else 0.0)   # most busy time
     r = det[k]
     rec = {"kernel": k, "fetch_kib": r["fetch_kib"], "write_kib": r["write_kib"], "fetch_factor": r["fetch_factor"],
@@ -291,6 +294,8 @@ def main(argv=None):
     ap.add_argument("--csv", help="per-kernel CSV output")
     ap.add_argument("--traffic-json", help="record the INT8 GEMM's HBM bytes per launch in this JSON file")
     ap.add_argument("--traffic-key", default="uniform", help="workload key of that record")
+    ap.add_argument("--traffic-stage", default="i8_gemm", choices=["i8_gemm", "prep"],
+                    help="stage whose busiest kernel the record is for")
     report(ap.parse_args(argv))
 
 

@@ -129,6 +129,27 @@ def test_traffic_json_record(tmp_path):
     assert rec["traffic_bytes"] == round((400 + 64) * 1024)
 
 
+def test_traffic_json_record_prep(tmp_path):
+    """--traffic-stage prep records prep's bytes per launch instead (the roofline kernel of a call
+    whose prep outlasts its INT8 GEMM), under the profiler's kernel name."""
+    rr = _tool()
+    tr = tmp_path / "t.csv"
+    _trace(tr, TIMELINE)
+    fe, wr, cf, cw = (tmp_path / f for f in ("fe.csv", "wr.csv", "cf.csv", "cw.csv"))
+    _counters(fe, "FETCH_SIZE", [(I8, 100.0), (PREP, 50.0), (PREP, 70.0)])
+    _counters(wr, "WRITE_SIZE", [(I8, 64.0), (PREP, 32.0)])
+    _counters(cf, "FETCH_SIZE", [(COPY, 524288.0)])
+    _counters(cw, "WRITE_SIZE", [(COPY, 1048576.0)])
+    js = tmp_path / "hbm.json"
+    rr.main([str(tr), "--fetch", str(fe), "--write", str(wr), "--copy-fetch", str(cf), "--copy-write", str(cw),
+             "-o", str(tmp_path / "r.md"), "--traffic-json", str(js), "--traffic-key", "hard",
+             "--traffic-stage", "prep"])
+    rec = rr.json.loads(js.read_text())["hard"]
+    assert rec["kernel"] == rr.short_name(PREP)
+    assert rec["fetch_kib"] == pytest.approx(60.0) and rec["write_kib"] == pytest.approx(32.0)
+    assert rec["traffic_bytes"] == round((120 + 32) * 1024)
+
+
 def test_dot_pass_counts_in_reconstruct_without_roofline(tmp_path):
     """The flagged entries' FP64 dot products (dots_kernel) run after recon_kernel: their time is
     reconstruct time, but the stage's algorithmic bytes are credited to recon_kernel alone."""
