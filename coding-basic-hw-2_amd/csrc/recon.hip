@@ -845,7 +845,8 @@ __device__ __forceinline__ void sparse_dots(const oz2_problem& pr, int r0, int c
 }
 
 // (launch bounds: seven waves per SIMD, which the summaries' partner loads and the chains' latency
-// need, at a few spilled registers; six: 3-6 % slower on the hard config)
+// need, at a few spilled registers; six: 3-6 % slower on 32 x 2048^3 + 4 x 2048^2 x 65536 products
+// with 0.1 % NaN / Inf entries)
 __global__ void __launch_bounds__(kThreads, 7) dots_kernel(const oz2_problem* __restrict__ probs,
                                                         const YDesc* __restrict__ yds, int gne, int gper, int form) {
   __shared__ __attribute__((aligned(16))) double buf[kUnion];
